@@ -1,0 +1,166 @@
+"""ctypes binding of the CPU oracle (``oracle/mxfp8_oracle.c``).
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py``, always as the checker or the
+timed CPU baseline, never as a product path. See ``mxfp8_oracle.h`` for the
+reference file:line each function restates.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libmxfp8_oracle.so")
+_lib = None
+
+D = 128
+
+
+def build():
+    """Compile the oracle (gcc, no GPU needed)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+class Problem(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int), ("H", ctypes.c_int), ("HK", ctypes.c_int), ("S", ctypes.c_int), ("SK", ctypes.c_int),
+                ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+                ("qs", ctypes.c_void_p), ("ks", ctypes.c_void_p), ("vdescale", ctypes.c_float), ("causal", ctypes.c_int)]
+
+
+class CheckResult(ctypes.Structure):
+    _fields_ = [("checked", ctypes.c_uint64), ("bad", ctypes.c_uint64), ("worst_err", ctypes.c_double),
+                ("mean_err", ctypes.c_double), ("max_ref", ctypes.c_double)]
+
+    def as_dict(self):
+        return {"checked": int(self.checked), "bad": int(self.bad), "worst_err": float(self.worst_err),
+                "mean_err": float(self.mean_err), "max_ref": float(self.max_ref)}
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        vp, i, f, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+        L.mxo_e4m3_decode.restype = ctypes.c_double
+        L.mxo_e4m3_decode.argtypes = [ctypes.c_uint8]
+        L.mxo_e4m3_encode_sat.restype = ctypes.c_uint8
+        L.mxo_e4m3_encode_sat.argtypes = [f]
+        L.mxo_cvt_bf16_fp8.restype = ctypes.c_uint8
+        L.mxo_cvt_bf16_fp8.argtypes = [ctypes.c_uint16, f]
+        L.mxo_pknorm_u16.restype = ctypes.c_uint16
+        L.mxo_pknorm_u16.argtypes = [f]
+        L.mxo_f32_to_f16.restype = ctypes.c_uint16
+        L.mxo_f32_to_f16.argtypes = [f]
+        L.mxo_f16_to_f32.restype = f
+        L.mxo_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.mxo_qs_bytes.restype = sz
+        L.mxo_qs_bytes.argtypes = [i, i, i]
+        L.mxo_ks_bytes.restype = sz
+        L.mxo_ks_bytes.argtypes = [i, i, i, i]
+        L.mxo_generate.restype = f
+        L.mxo_generate.argtypes = [i, i, i, i, i, i, ctypes.c_uint64, vp, vp, vp, vp, vp]
+        L.mxo_select_path.restype = i
+        L.mxo_select_path.argtypes = [ctypes.c_long] * 4 + [ctypes.POINTER(i)]
+        L.mxo_split_range.restype = None
+        L.mxo_split_range.argtypes = [i, i, i, ctypes.POINTER(i), ctypes.POINTER(i)]
+        L.mxo_check_fp64.restype = CheckResult
+        L.mxo_check_fp64.argtypes = [ctypes.POINTER(Problem), vp, i, i]
+        L.mxo_attention_fp32.restype = ctypes.c_double
+        L.mxo_attention_fp32.argtypes = [ctypes.POINTER(Problem), i, vp, i]
+        L.mxo_emulate.restype = None
+        L.mxo_emulate.argtypes = [ctypes.POINTER(Problem), i, i, vp, vp, vp, i]
+        L.mxo_combine.restype = None
+        L.mxo_combine.argtypes = [vp, vp, vp, ctypes.c_long, i]
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+MODES = {"lcg": 0, "uniform": 1, "normal": 2}
+
+
+class Inputs:
+    """Seeded MXFP8 inputs in the reference layout (ref_host.cpp:183-263), host numpy arrays."""
+
+    def __init__(self, B, H, S, SK, HK=None, mode="normal", seed_mix=0, causal=False):
+        HK = HK or H
+        self.B, self.H, self.HK, self.S, self.SK, self.causal = B, H, HK, S, SK, bool(causal)
+        L = lib()
+        self.q = np.zeros(B * S * H * D, np.uint8)
+        self.k = np.zeros(B * SK * HK * D, np.uint8)
+        self.v = np.zeros(B * SK * HK * D, np.uint8)
+        self.qs = np.zeros(L.mxo_qs_bytes(B, H, S), np.uint8)
+        self.ks = np.zeros(L.mxo_ks_bytes(B, H, HK, SK), np.uint8)
+        self.vdescale = float(L.mxo_generate(MODES[mode], B, H, HK, S, SK, seed_mix, _ptr(self.q), _ptr(self.k),
+                                             _ptr(self.v), _ptr(self.qs), _ptr(self.ks)))
+        self.vd_buf = np.zeros(1024, np.float32)
+        self.vd_buf[0] = self.vdescale
+
+    def problem(self):
+        p = Problem(self.B, self.H, self.HK, self.S, self.SK, _ptr(self.q).value, _ptr(self.k).value, _ptr(self.v).value,
+                    _ptr(self.qs).value, _ptr(self.ks).value, self.vdescale, int(self.causal))
+        return p
+
+    @property
+    def out_elems(self):
+        return self.B * self.S * self.H * D
+
+
+def check_fp64(inp, out_bf16, rows=64, threads=0):
+    """ref_host.cpp:436-471 statistics of a bf16 output (uint16 array)."""
+    out = np.ascontiguousarray(out_bf16, dtype=np.uint16).reshape(-1)
+    assert out.size == inp.out_elems
+    p = inp.problem()
+    return lib().mxo_check_fp64(ctypes.byref(p), _ptr(out), int(rows), int(threads)).as_dict()
+
+
+def emulate(inp, splits=0, rows=64, threads=0, partials=False):
+    """Bit-level model of the reference kernels on the first ``rows`` rows of every (b, h).
+    Returns the bf16 output (uint16, rows not emulated are 0), and with ``partials`` also (ohat fp16, lse f32)."""
+    out = np.zeros(inp.out_elems, np.uint16)
+    ohat = lse = None
+    if partials and splits:
+        rows_total = inp.B * inp.S * inp.H
+        ohat = np.zeros(splits * rows_total * D, np.uint16)
+        lse = np.zeros(splits * rows_total, np.float32)
+    p = inp.problem()
+    lib().mxo_emulate(ctypes.byref(p), int(splits), int(rows), _ptr(out), _ptr(ohat), _ptr(lse), int(threads))
+    return (out, ohat, lse) if partials else out
+
+
+def attention_fp32(inp, rows=0, threads=0, want_out=True):
+    """fp32 attention on the dequantised inputs (the CPU baseline). Returns (seconds, out or None)."""
+    out = np.zeros(inp.out_elems, np.float32) if want_out else None
+    p = inp.problem()
+    secs = lib().mxo_attention_fp32(ctypes.byref(p), int(rows), _ptr(out), int(threads))
+    return secs, out
+
+
+def select_path(B, H, S, SK):
+    sp = ctypes.c_int(0)
+    path = lib().mxo_select_path(B, H, S, SK, ctypes.byref(sp))
+    return ("vs128", "t128", "kvsplit")[path], sp.value
+
+
+def split_range(SK, splits, s):
+    lo, n = ctypes.c_int(0), ctypes.c_int(0)
+    lib().mxo_split_range(SK, splits, s, ctypes.byref(lo), ctypes.byref(n))
+    return lo.value, n.value
+
+
+def combine(ohat, lse, rows_total, splits):
+    out = np.zeros(rows_total * D, np.uint16)
+    lib().mxo_combine(_ptr(np.ascontiguousarray(ohat, np.uint16)), _ptr(np.ascontiguousarray(lse, np.float32)), _ptr(out),
+                      rows_total, splits)
+    return out
+
+
+def bf16_to_f32(a):
+    return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
