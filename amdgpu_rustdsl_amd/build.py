@@ -1,0 +1,49 @@
+"""Build of the native library: the gfx950 code object and the C-ABI host library that embeds it.
+
+    python -m amdgpu_rustdsl_amd.build          # or __graft_entry__.build()
+
+Outputs (in-tree, git-ignored, shipped with the source tree):
+    amdgpu_rustdsl_amd/_build/fmha_mxfp8_gfx950.hsaco   the four kernels (hipcc --genco, gfx950 only)
+    amdgpu_rustdsl_amd/_build/libfmha_mxfp8.so          include/fmha_mxfp8.h, code object embedded
+"""
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+OUT = os.path.join(PKG, "_build")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HSACO = os.path.join(OUT, "fmha_mxfp8_gfx950.hsaco")
+LIB = os.path.join(OUT, "libfmha_mxfp8.so")
+
+# Packed FP32 VALU forms are kept out of the kernels (their results have been unreliable on this hardware pool);
+# the host pass warns that it does not know the feature, which is harmless.
+HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-command-line-argument"]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("build step failed: " + " ".join(cmd))
+    return r
+
+
+def build(verbose=False):
+    os.makedirs(OUT, exist_ok=True)
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    _run([hipcc, *HIP_FLAGS, "--genco", os.path.join(CSRC, "fmha_kernels.hip"), "-o", HSACO])
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+          "-I" + os.path.join(ROCM, "include"), '-DFMHA_HSACO_PATH="%s"' % HSACO,
+          os.path.join(CSRC, "fmha_host.cpp"), "-L" + os.path.join(ROCM, "lib"), "-lamdhip64",
+          "-Wl,-rpath," + os.path.join(ROCM, "lib"), "-o", LIB])
+    if verbose:
+        print("built", HSACO, os.path.getsize(HSACO), "bytes;", LIB, os.path.getsize(LIB), "bytes")
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose=True)

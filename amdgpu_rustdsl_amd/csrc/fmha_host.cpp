@@ -1,0 +1,442 @@
+// fmha_host.cpp - host side of the MXFP8 FMHA forward: the C ABI of include/fmha_mxfp8.h.
+//
+// The host contract (validate), the dispatch rule, the kernarg filling and the launches through
+// hipModuleLaunchKernel with HIP_LAUNCH_PARAM_BUFFER_POINTER, exactly the way the reference's generated
+// headers launch its kernels (tests/gpu/generated/fmha_fwd_hd128_mxfp8_v3_vs128_abi.h:204-209). The gfx950
+// code object (fmha_kernels.hip) is embedded in this library at build time and loaded once per device with
+// hipModuleLoadData. No function allocates device memory; the KV-split workspace is the caller's.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <atomic>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/fmha_mxfp8.h"
+
+static_assert(sizeof(fmha_mxfp8_args) == 656, "kernarg size (vs128_abi.h:126)");
+static_assert(offsetof(fmha_mxfp8_args, ptr_o) == 0x000, "ptr_o");
+static_assert(offsetof(fmha_mxfp8_args, ptr_q) == 0x010, "ptr_q");
+static_assert(offsetof(fmha_mxfp8_args, ptr_k) == 0x020, "ptr_k");
+static_assert(offsetof(fmha_mxfp8_args, ptr_v) == 0x030, "ptr_v");
+static_assert(offsetof(fmha_mxfp8_args, ptr_lse) == 0x040, "ptr_lse");
+static_assert(offsetof(fmha_mxfp8_args, softmax_scale) == 0x050, "scale");
+static_assert(offsetof(fmha_mxfp8_args, s_seq_len) == 0x060, "s_seq_len");
+static_assert(offsetof(fmha_mxfp8_args, s_Seqs) == 0x070, "s_Seqs");
+static_assert(offsetof(fmha_mxfp8_args, s_Hs) == 0x090, "s_Hs");
+static_assert(offsetof(fmha_mxfp8_args, s_Bs) == 0x0A0, "s_Bs");
+static_assert(offsetof(fmha_mxfp8_args, s_gqa) == 0x0B0, "s_gqa");
+static_assert(offsetof(fmha_mxfp8_args, s_k_Seqs) == 0x0C0, "s_k_Seqs");
+static_assert(offsetof(fmha_mxfp8_args, s_k_Hs) == 0x0D0, "s_k_Hs");
+static_assert(offsetof(fmha_mxfp8_args, s_k_Bs) == 0x0E0, "s_k_Bs");
+static_assert(offsetof(fmha_mxfp8_args, opt) == 0x0F0, "opt");
+static_assert(offsetof(fmha_mxfp8_args, s_kv_seq_len) == 0x110, "s_kv_seq_len");
+static_assert(offsetof(fmha_mxfp8_args, s_q_head_num) == 0x140, "s_q_head_num");
+static_assert(offsetof(fmha_mxfp8_args, s_v_Seqs) == 0x150, "s_v_Seqs");
+static_assert(offsetof(fmha_mxfp8_args, s_v_Hs) == 0x160, "s_v_Hs");
+static_assert(offsetof(fmha_mxfp8_args, s_v_Bs) == 0x170, "s_v_Bs");
+static_assert(offsetof(fmha_mxfp8_args, s_o_Seqs) == 0x180, "s_o_Seqs");
+static_assert(offsetof(fmha_mxfp8_args, s_o_Hs) == 0x190, "s_o_Hs");
+static_assert(offsetof(fmha_mxfp8_args, s_o_Bs) == 0x1A0, "s_o_Bs");
+static_assert(offsetof(fmha_mxfp8_args, ptr_q_descale) == 0x200, "ptr_q_descale");
+static_assert(offsetof(fmha_mxfp8_args, ptr_k_descale) == 0x210, "ptr_k_descale");
+static_assert(offsetof(fmha_mxfp8_args, ptr_v_descale) == 0x220, "ptr_v_descale");
+static_assert(offsetof(fmha_mxfp8_args, s_descale_q_Bs) == 0x230, "s_descale_q_Bs");
+static_assert(offsetof(fmha_mxfp8_args, s_descale_q_Hs) == 0x240, "s_descale_q_Hs");
+static_assert(offsetof(fmha_mxfp8_args, s_descale_k_Bs) == 0x250, "s_descale_k_Bs");
+static_assert(offsetof(fmha_mxfp8_args, s_descale_k_Hs) == 0x260, "s_descale_k_Hs");
+static_assert(offsetof(fmha_mxfp8_args, flags) == 0x280, "flags / abi_tail");
+static_assert(sizeof(fmha_mxfp8_kvsplit_args) == 648, "kvsplit kernarg size (kvsplit_abi.h:136)");
+static_assert(offsetof(fmha_mxfp8_kvsplit_args, ptr_ohat) == 0x270, "ptr_ohat");
+static_assert(offsetof(fmha_mxfp8_kvsplit_args, ptr_lse) == 0x278, "ptr_lse");
+static_assert(offsetof(fmha_mxfp8_kvsplit_args, kvs_splits) == 0x280, "kvs_splits");
+static_assert(offsetof(fmha_mxfp8_kvsplit_args, kvs_rows_total) == 0x284, "kvs_rows_total");
+static_assert(sizeof(fmha_mxfp8_combine_args) == 36, "combine kernarg size (combine8h_abi.h:34)");
+static_assert(offsetof(fmha_mxfp8_combine_args, rows_total) == 0x18, "rows_total");
+static_assert(offsetof(fmha_mxfp8_combine_args, splits) == 0x20, "splits");
+
+// The code object, embedded by the build (FMHA_HSACO_PATH names the file built from fmha_kernels.hip).
+#ifndef FMHA_HSACO_PATH
+#error "FMHA_HSACO_PATH must name the gfx950 code object built from fmha_kernels.hip"
+#endif
+asm(".section .rodata.fmha_hsaco,\"a\",@progbits\n"
+    ".balign 4096\n"
+    ".global fmha_mxfp8_hsaco_begin\n"
+    "fmha_mxfp8_hsaco_begin:\n"
+    ".incbin \"" FMHA_HSACO_PATH "\"\n"
+    ".global fmha_mxfp8_hsaco_end\n"
+    "fmha_mxfp8_hsaco_end:\n"
+    ".previous\n");
+extern "C" const unsigned char fmha_mxfp8_hsaco_begin[];
+extern "C" const unsigned char fmha_mxfp8_hsaco_end[];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+const char* const kKernelNames[4] = {
+    "fmha_fwd_hd128_mxfp8_v3_vs128",
+    "fmha_fwd_hd128_mxfp8_v3_t128",
+    "fmha_fwd_hd128_mxfp8_v3_kvsplit",
+    "fmha_fwd_hd128_mxfp8_v3_kvsplit_combine8h",
+};
+enum { K_VS128 = 0, K_T128 = 1, K_KVSPLIT = 2, K_COMBINE = 3 };
+
+struct DeviceModule {
+    std::atomic<bool> loaded{false};
+    hipModule_t mod = nullptr;
+    hipFunction_t fn[4] = {nullptr, nullptr, nullptr, nullptr};
+};
+DeviceModule g_dev[kMaxDevices];
+std::mutex g_mu;
+
+void set_err(char* err, size_t errlen, const char* fmt, ...) {
+    if (!err || errlen == 0) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, errlen, fmt, ap);
+    va_end(ap);
+}
+
+int fail(char* err, size_t errlen, int code, const char* prefix, const char* msg) {
+    set_err(err, errlen, "%s: %s", prefix, msg);
+    return code;
+}
+
+// Loads the embedded code object on the current device (once per device, thread-safe).
+int get_functions(hipFunction_t** out, char* err, size_t errlen) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        set_err(err, errlen, "hipGetDevice: %s", hipGetErrorString(e));
+        return FMHA_ERR_NO_DEVICE;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_err(err, errlen, "device %d out of range", dev);
+        return FMHA_ERR_NO_DEVICE;
+    }
+    DeviceModule& dm = g_dev[dev];
+    if (!dm.loaded.load(std::memory_order_acquire)) {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (!dm.loaded.load(std::memory_order_relaxed)) {
+            hipModule_t mod = nullptr;
+            e = hipModuleLoadData(&mod, fmha_mxfp8_hsaco_begin);
+            if (e != hipSuccess) {
+                set_err(err, errlen, "hipModuleLoadData (gfx950 code object, %zu bytes): %s",
+                        (size_t)(fmha_mxfp8_hsaco_end - fmha_mxfp8_hsaco_begin), hipGetErrorString(e));
+                return FMHA_ERR_NO_DEVICE;
+            }
+            for (int i = 0; i < 4; ++i) {
+                e = hipModuleGetFunction(&dm.fn[i], mod, kKernelNames[i]);
+                if (e != hipSuccess) {
+                    set_err(err, errlen, "hipModuleGetFunction(%s): %s", kKernelNames[i], hipGetErrorString(e));
+                    hipModuleUnload(mod);
+                    return FMHA_ERR_NO_DEVICE;
+                }
+            }
+            dm.mod = mod;
+            dm.loaded.store(true, std::memory_order_release);
+        }
+    }
+    *out = dm.fn;
+    return FMHA_OK;
+}
+
+int launch_raw(int which, const void* args, size_t nbytes, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block,
+               void* stream, char* err, size_t errlen) {
+    hipFunction_t* fns = nullptr;
+    int rc = get_functions(&fns, err, errlen);
+    if (rc != FMHA_OK) return rc;
+    size_t sz = nbytes;
+    void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(args), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+                     HIP_LAUNCH_PARAM_END};
+    hipError_t e = hipModuleLaunchKernel(fns[which], gx, gy, gz, block, 1, 1, 0, (hipStream_t)stream, nullptr, extra);
+    if (e != hipSuccess) {
+        set_err(err, errlen, "hipModuleLaunchKernel(%s): %s", kKernelNames[which], hipGetErrorString(e));
+        return FMHA_ERR_HIP;
+    }
+    return FMHA_OK;
+}
+
+typedef long long i64;
+
+// The 0x000-0x26F rules shared by vs128 / t128 / kvsplit (vs128_abi.h:170-203), in the reference's four groups
+// and order: buffer extents, kernarg ranges, kernarg relations, grid. `B` is grid.z for the single-kernel launches
+// and the host symbol B for the KV split (kvsplit_abi.h).
+int rules_extent(const fmha_mxfp8_args& a, const fmha_mxfp8_buffer_sizes& sz, i64 B, char* err, size_t errlen) {
+    const i64 H = a.s_q_head_num;
+    if (sz.ptr_q < (uint64_t)(B * (i64)a.s_Bs)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_q: buffer ptr_q smaller than declared allocation");
+    if (sz.ptr_k < (uint64_t)(B * (i64)a.s_k_Bs)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_k: buffer ptr_k smaller than declared allocation");
+    if (sz.ptr_v < (uint64_t)(B * (i64)a.s_v_Bs)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_v: buffer ptr_v smaller than declared allocation");
+    if (sz.ptr_o < (uint64_t)(B * (i64)a.s_o_Bs)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_o: buffer ptr_o smaller than declared allocation");
+    if (sz.ptr_q_descale < (uint64_t)(B * (i64)a.s_descale_q_Bs + 2048LL * H))
+        return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_q_descale: buffer ptr_q_descale smaller than declared allocation");
+    if (sz.ptr_k_descale < (uint64_t)(B * (i64)a.s_descale_k_Bs + 2560LL * H))
+        return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_k_descale: buffer ptr_k_descale smaller than declared allocation");
+    if (sz.ptr_v_descale < 4096ull) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_v_descale: buffer ptr_v_descale smaller than declared allocation");
+    return FMHA_OK;
+}
+
+int rules_range(const fmha_mxfp8_args& a, char* err, size_t errlen) {
+    const i64 gqa = a.s_gqa;
+    if (gqa < 1 || gqa > 16) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0xB0) outside contract");
+    if (a.s_seq_len < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x60) outside contract");
+    if (a.s_kv_seq_len < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x110) outside contract");
+    if (a.s_Hs != 128) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x90) outside contract");
+    if (a.s_k_Hs != 128) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0xD0) outside contract");
+    if (a.s_v_Hs != 128) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x160) outside contract");
+    if (a.s_o_Hs != 256) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x190) outside contract");
+    if (a.s_descale_q_Hs != 4) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x240) outside contract");
+    if (a.s_descale_k_Hs != 4) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x260) outside contract");
+    return FMHA_OK;
+}
+
+int rules_is(const fmha_mxfp8_args& a, i64 HK, char* err, size_t errlen) {
+    const i64 S = a.s_seq_len, SK = a.s_kv_seq_len, H = a.s_q_head_num;
+    if (H != HK * (i64)a.s_gqa) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0x140) relation failed");
+    if ((i64)a.s_Seqs != H * 128) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0x70) relation failed");
+    if ((i64)a.s_Bs != S * (i64)a.s_Seqs) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0xA0) relation failed");
+    if ((i64)a.s_k_Seqs != HK * 128) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0xC0) relation failed");
+    if ((i64)a.s_k_Bs != SK * (i64)a.s_k_Seqs) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0xE0) relation failed");
+    if (a.s_v_Seqs != a.s_k_Seqs) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0x150) relation failed");
+    if (a.s_v_Bs != a.s_k_Bs) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0x170) relation failed");
+    if ((i64)a.s_o_Seqs != H * 256) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0x180) relation failed");
+    if ((i64)a.s_o_Bs != S * (i64)a.s_o_Seqs) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0x1A0) relation failed");
+    if ((i64)a.s_descale_q_Bs != S * H * 4) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0x230) relation failed");
+    if ((i64)a.s_descale_k_Bs != SK * HK * 4) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0x250) relation failed");
+    return FMHA_OK;
+}
+
+int rules_grid(const fmha_mxfp8_args& a, uint32_t gx, uint32_t gy, int rows_per_block, char* err, size_t errlen) {
+    if ((i64)gy != (i64)a.s_q_head_num) return fail(err, errlen, FMHA_ERR_GRID, "GV-HOST-GRID", "grid axis 1 relation failed");
+    if ((i64)gx != ((i64)a.s_seq_len + rows_per_block - 1) / rows_per_block)
+        return fail(err, errlen, FMHA_ERR_GRID, "GV-HOST-GRID", "grid axis 0 relation failed");
+    return FMHA_OK;
+}
+
+int validate_base(const fmha_mxfp8_args& a, const fmha_mxfp8_buffer_sizes& sz, uint32_t gx, uint32_t gy, i64 B, i64 HK,
+                  int rows_per_block, char* err, size_t errlen) {
+    int rc;
+    if ((rc = rules_extent(a, sz, B, err, errlen)) != FMHA_OK) return rc;
+    if ((rc = rules_range(a, err, errlen)) != FMHA_OK) return rc;
+    if ((rc = rules_is(a, HK, err, errlen)) != FMHA_OK) return rc;
+    return rules_grid(a, gx, gy, rows_per_block, err, errlen);
+}
+
+bool empty_split(i64 SK, i64 splits) {
+    const i64 ntiles = (SK + 127) / 128;
+    const i64 tps = (ntiles + splits - 1) / splits;
+    return !((splits - 1) * tps < ntiles);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fmha_mxfp8_version(void) { return "fmha_mxfp8 gfx950 1.0"; }
+
+int fmha_mxfp8_init(char* err, size_t errlen) {
+    hipFunction_t* fns = nullptr;
+    return get_functions(&fns, err, errlen);
+}
+
+int fmha_mxfp8_validate_vs128(const fmha_mxfp8_args* a, const fmha_mxfp8_buffer_sizes* sz, uint32_t gx, uint32_t gy,
+                              uint32_t gz, int64_t HK, char* err, size_t errlen) {
+    return validate_base(*a, *sz, gx, gy, (i64)gz, HK, 256, err, errlen);
+}
+
+int fmha_mxfp8_validate_t128(const fmha_mxfp8_args* a, const fmha_mxfp8_buffer_sizes* sz, uint32_t gx, uint32_t gy,
+                             uint32_t gz, int64_t HK, char* err, size_t errlen) {
+    return validate_base(*a, *sz, gx, gy, (i64)gz, HK, 128, err, errlen);
+}
+
+int fmha_mxfp8_validate_kvsplit(const fmha_mxfp8_kvsplit_args* ka, const fmha_mxfp8_buffer_sizes* sz, uint32_t gx,
+                                uint32_t gy, uint32_t gz, int64_t B, int64_t HK, int64_t KL, char* err, size_t errlen) {
+    // kvsplit_abi.h: the base rules with the symbol B, the split extension inserted into each group
+    fmha_mxfp8_args a;
+    std::memcpy(&a, ka, 0x270);
+    std::memset(reinterpret_cast<uint8_t*>(&a) + 0x270, 0, sizeof(a) - 0x270);
+    const i64 splits = ka->kvs_splits, rows = ka->kvs_rows_total;
+    int rc;
+    if ((rc = rules_extent(a, *sz, B, err, errlen)) != FMHA_OK) return rc;
+    if (sz->ptr_ohat < (uint64_t)(splits * rows * 512)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_ohat: buffer ptr_ohat smaller than declared allocation");
+    if (sz->ptr_lse < (uint64_t)(splits * rows * 4)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_lse: buffer ptr_lse smaller than declared allocation");
+    if ((rc = rules_range(a, err, errlen)) != FMHA_OK) return rc;
+    if (splits < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x280) outside contract");
+    if (rows < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x284) outside contract");
+    if ((rc = rules_is(a, HK, err, errlen)) != FMHA_OK) return rc;
+    if (rows != B * (i64)a.s_seq_len * (i64)a.s_q_head_num) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0x284) relation failed");
+    if ((rc = rules_grid(a, gx, gy, 256, err, errlen)) != FMHA_OK) return rc;
+    if ((i64)gz != B * splits) return fail(err, errlen, FMHA_ERR_GRID, "GV-HOST-GRID", "grid axis 2 relation failed");
+    if (KL < 0) return fail(err, errlen, FMHA_ERR_SYM, "GV-HOST-SYM", "symbol KL outside contract");
+    return FMHA_OK;
+}
+
+int fmha_mxfp8_validate_combine(const fmha_mxfp8_combine_args* a, const fmha_mxfp8_buffer_sizes* sz, uint32_t gx,
+                                uint32_t gy, uint32_t gz, char* err, size_t errlen) {
+    // combine8h_abi.h:56-65
+    (void)gx; (void)gy; (void)gz;
+    const i64 rows = a->rows_total, splits = a->splits;
+    if (sz->ptr_ohat < (uint64_t)(splits * rows * 512)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_ohat: buffer ptr_ohat smaller than declared allocation");
+    if (sz->ptr_lse < (uint64_t)(splits * rows * 4)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_lse: buffer ptr_lse smaller than declared allocation");
+    if (sz->ptr_o < (uint64_t)(rows * 256)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_out: buffer ptr_out smaller than declared allocation");
+    if (rows < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x18) outside contract");
+    if (a->d != 128) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x1C) outside contract");
+    if (splits < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x20) outside contract");
+    return FMHA_OK;
+}
+
+int fmha_mxfp8_select_path(int64_t B, int64_t H, int64_t S, int64_t SK, int* splits) {
+    // dispatch.rs:494-511
+    const i64 blocks256 = (S + 255) / 256 * H * B;
+    const i64 ntiles = (SK + 127) / 128;
+    i64 sp = 0;
+    if (ntiles >= 16 && blocks256 <= 64) sp = 4;
+    else if (ntiles >= 32 && blocks256 <= 128) sp = 2;
+    if (sp > 0 && !empty_split(SK, sp)) {
+        if (splits) *splits = (int)sp;
+        return FMHA_PATH_KVSPLIT;
+    }
+    if (splits) *splits = 0;
+    return blocks256 <= 64 ? FMHA_PATH_T128 : FMHA_PATH_VS128;
+}
+
+void fmha_mxfp8_fill_args(fmha_mxfp8_args* a, void* o, const void* q, const void* k, const void* v, const void* q_descale,
+                          const void* k_descale, const void* v_descale, int B, int H, int HK, int S, int SK) {
+    // the values tests/gpu/ref_host.cpp:342-360 writes
+    (void)B;
+    std::memset(a, 0, sizeof(*a));
+    const uint32_t D = 128;
+    a->ptr_o = o;
+    a->ptr_q = const_cast<void*>(q);
+    a->ptr_k = const_cast<void*>(k);
+    a->ptr_v = const_cast<void*>(v);
+    a->s_seq_len = (uint32_t)S;
+    a->s_Seqs = (uint32_t)H * D;
+    a->s_Hs = D;
+    a->s_Bs = (uint32_t)((uint64_t)S * H * D);
+    a->s_gqa = (uint32_t)(H / HK);
+    a->s_k_Seqs = (uint32_t)HK * D;
+    a->s_k_Hs = D;
+    a->s_k_Bs = (uint32_t)((uint64_t)SK * HK * D);
+    a->s_kv_seq_len = (uint32_t)SK;
+    a->s_q_head_num = (uint32_t)H;
+    a->s_v_Seqs = (uint32_t)HK * D;
+    a->s_v_Hs = D;
+    a->s_v_Bs = (uint32_t)((uint64_t)SK * HK * D);
+    a->s_o_Seqs = (uint32_t)H * D * 2;
+    a->s_o_Hs = D * 2;
+    a->s_o_Bs = (uint32_t)((uint64_t)S * H * D * 2);
+    a->ptr_q_descale = const_cast<void*>(q_descale);
+    a->ptr_k_descale = const_cast<void*>(k_descale);
+    a->ptr_v_descale = const_cast<void*>(v_descale);
+    a->s_descale_q_Bs = (uint32_t)((uint64_t)S * H * 4);
+    a->s_descale_q_Hs = 4;
+    a->s_descale_k_Bs = (uint32_t)((uint64_t)SK * HK * 4);
+    a->s_descale_k_Hs = 4;
+    const float scale = 0.08838834764831845f;   // 1/sqrt(128), written as the reference host does (ignored)
+    std::memcpy(&a->softmax_scale, &scale, 4);
+}
+
+size_t fmha_mxfp8_workspace_bytes(int64_t B, int64_t H, int64_t S, int splits) {
+    if (splits <= 0) return 0;
+    const uint64_t rows = (uint64_t)B * (uint64_t)S * (uint64_t)H;
+    return (size_t)((uint64_t)splits * rows * (512u + 4u));
+}
+
+int fmha_mxfp8_launch_vs128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream) {
+    return launch_raw(K_VS128, a, sizeof(*a), gx, gy, gz, 512, stream, nullptr, 0);
+}
+int fmha_mxfp8_launch_t128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream) {
+    return launch_raw(K_T128, a, sizeof(*a), gx, gy, gz, 256, stream, nullptr, 0);
+}
+int fmha_mxfp8_launch_kvsplit(const fmha_mxfp8_kvsplit_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream) {
+    return launch_raw(K_KVSPLIT, a, sizeof(*a), gx, gy, gz, 512, stream, nullptr, 0);
+}
+int fmha_mxfp8_launch_combine(const fmha_mxfp8_combine_args* a, uint32_t gx, void* stream) {
+    return launch_raw(K_COMBINE, a, sizeof(*a), gx, 1, 1, 256, stream, nullptr, 0);
+}
+
+int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_t workspace_bytes, void* stream, int* path_out,
+                              int* splits_out, char* err, size_t errlen) {
+    if (!p) return fail(err, errlen, FMHA_ERR_PATH, "GV-HOST-ARGS", "null params");
+    const i64 B = p->B, H = p->H, HK = p->HK, S = p->S, SK = p->SK;
+    if (B < 1 || H < 1 || HK < 1 || S < 1 || SK < 1)
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "B, H, HK, S, SK must be >= 1");
+    if (H % HK != 0 || ((H / HK) & (H / HK - 1)) != 0 || H / HK > 16)
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "H must be a power-of-two multiple (<= 16) of HK");
+    int splits = 0;
+    int path = p->path;
+    if (path < 0) {
+        path = fmha_mxfp8_select_path(B, H, S, SK, &splits);
+        if (p->causal && path == FMHA_PATH_KVSPLIT) path = ((S + 255) / 256 * H * B <= 64) ? FMHA_PATH_T128 : FMHA_PATH_VS128;
+    } else if (path == FMHA_PATH_KVSPLIT) {
+        splits = p->splits > 0 ? p->splits : 4;
+    }
+    if (path != FMHA_PATH_VS128 && path != FMHA_PATH_T128 && path != FMHA_PATH_KVSPLIT)
+        return fail(err, errlen, FMHA_ERR_PATH, "GV-HOST-PATH", "unknown path");
+    if (path == FMHA_PATH_KVSPLIT) {
+        if (splits != 2 && splits != 4 && splits != 8) return fail(err, errlen, FMHA_ERR_PATH, "GV-HOST-PATH", "KV split count must be 2, 4 or 8");
+        if (empty_split(SK, splits)) return fail(err, errlen, FMHA_ERR_PATH, "GV-HOST-PATH", "KV split leaves a split without a key tile");
+        if (p->causal) return fail(err, errlen, FMHA_ERR_PATH, "GV-HOST-PATH", "the causal mask is not supported on the KV-split path");
+    }
+    fmha_mxfp8_args a;
+    fmha_mxfp8_fill_args(&a, p->o, p->q, p->k, p->v, p->q_descale, p->k_descale, p->v_descale, (int)B, (int)H, (int)HK, (int)S, (int)SK);
+    a.flags = p->causal ? 1u : 0u;
+    fmha_mxfp8_buffer_sizes sz;
+    std::memset(&sz, 0, sizeof(sz));
+    sz.ptr_q = p->bytes_q; sz.ptr_k = p->bytes_k; sz.ptr_v = p->bytes_v; sz.ptr_o = p->bytes_o;
+    sz.ptr_q_descale = p->bytes_q_descale; sz.ptr_k_descale = p->bytes_k_descale; sz.ptr_v_descale = p->bytes_v_descale;
+    if (path_out) *path_out = path;
+    if (splits_out) *splits_out = path == FMHA_PATH_KVSPLIT ? splits : 0;
+    const uint32_t gy = (uint32_t)H;
+    if (path == FMHA_PATH_VS128 || path == FMHA_PATH_T128) {
+        a.ptr_lse = p->lse;
+        const int rows = path == FMHA_PATH_VS128 ? 256 : 128;
+        const uint32_t gx = (uint32_t)((S + rows - 1) / rows);
+        int rc = path == FMHA_PATH_VS128 ? fmha_mxfp8_validate_vs128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen)
+                                         : fmha_mxfp8_validate_t128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen);
+        if (rc != FMHA_OK) return rc;
+        return launch_raw(path == FMHA_PATH_VS128 ? K_VS128 : K_T128, &a, sizeof(a), gx, gy, (uint32_t)B, (uint32_t)(rows * 2), stream,
+                          err, errlen);
+    }
+    // KV split: partials (fp32-sized rows, as ref_host.cpp:149 / ops.py:133) then the LSE, both in the workspace
+    const i64 rows_total = B * S * H;
+    const size_t need = fmha_mxfp8_workspace_bytes(B, H, S, splits);
+    if (!workspace || workspace_bytes < need) {
+        set_err(err, errlen, "GV-HOST-WORKSPACE: KV split needs %zu workspace bytes, got %zu", need, workspace_bytes);
+        return FMHA_ERR_WORKSPACE;
+    }
+    uint8_t* ohat = (uint8_t*)workspace;
+    uint8_t* lse = ohat + (size_t)splits * rows_total * 512;
+    fmha_mxfp8_kvsplit_args ka;
+    std::memcpy(&ka, &a, 0x270);
+    ka.ptr_ohat = ohat;
+    ka.ptr_lse = lse;
+    ka.kvs_splits = (uint32_t)splits;
+    ka.kvs_rows_total = (uint32_t)rows_total;
+    sz.ptr_ohat = (uint64_t)splits * rows_total * 512;
+    sz.ptr_lse = (uint64_t)splits * rows_total * 4;
+    const uint32_t gx = (uint32_t)((S + 255) / 256), gz = (uint32_t)(B * splits);
+    int rc = fmha_mxfp8_validate_kvsplit(&ka, &sz, gx, gy, gz, B, HK, 0, err, errlen);
+    if (rc != FMHA_OK) return rc;
+    rc = launch_raw(K_KVSPLIT, &ka, sizeof(ka), gx, gy, gz, 512, stream, err, errlen);
+    if (rc != FMHA_OK) return rc;
+    fmha_mxfp8_combine_args ca;
+    ca.ptr_ohat = ohat;
+    ca.ptr_lse = lse;
+    ca.ptr_out = p->o;
+    ca.rows_total = (uint32_t)rows_total;
+    ca.d = 128;
+    ca.splits = (uint32_t)splits;
+    fmha_mxfp8_buffer_sizes csz = sz;
+    csz.ptr_o = p->bytes_o;
+    rc = fmha_mxfp8_validate_combine(&ca, &csz, 0, 1, 1, err, errlen);
+    if (rc != FMHA_OK) return rc;
+    const uint64_t cgrid = ((uint64_t)rows_total * 128 / 8 + 255) / 256;
+    return launch_raw(K_COMBINE, &ca, sizeof(ca), (uint32_t)(cgrid ? cgrid : 1), 1, 1, 256, stream, err, errlen);
+}
+
+}  // extern "C"

@@ -1,0 +1,151 @@
+"""The MXFP8 FMHA forward op on torch device tensors, mirroring the reference's ``fmha_fwd_mxfp8``
+(python/amdgpu_jit/ops.py:88-143): same arguments, layouts, path names and errors, over the C ABI of
+include/fmha_mxfp8.h (``amdgpu_rustdsl_amd.lib``). torch is used for device memory and the current stream only.
+"""
+import math
+
+import torch
+
+from . import lib
+
+D = 128
+FMHA_VS128 = "fmha_fwd_hd128_mxfp8_v3_vs128"
+FMHA_T128 = "fmha_fwd_hd128_mxfp8_v3_t128"
+FMHA_KVSPLIT = "fmha_fwd_hd128_mxfp8_v3_kvsplit"
+FMHA_COMBINE = "fmha_fwd_hd128_mxfp8_v3_kvsplit_combine8h"
+
+
+def select_path(B, H, S, SK):
+    """(path, splits) of the shipped dispatch (``dispatch::mxfp8_prefill_path``, dispatch.rs:494-511)."""
+    return lib.select_path(B, H, S, SK)
+
+
+def _cap(t):
+    """Bytes from the tensor's first element to the end of its storage (the allocation the kernel may touch)."""
+    return t.untyped_storage().nbytes() - t.storage_offset() * t.element_size()
+
+
+def _expect(t, name, shape, esize, align=1):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: expected a device tensor, got {t.device}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
+    if t.element_size() != esize:
+        raise ValueError(f"{name}: expected {esize}-byte elements, got {t.element_size()}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: expected a contiguous tensor")
+    if t.data_ptr() % align:
+        raise ValueError(f"{name}: expected {align}-byte alignment")
+
+
+_workspace = {}
+
+
+def _ws(device, stream, nbytes):
+    """Persistent KV-split workspace per (device, stream), grown on demand (ops.py:73-85)."""
+    key = (device, stream)
+    buf = _workspace.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = _workspace[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return buf
+
+
+def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", splits=None, stream=None, lse=None, causal=False):
+    """MXFP8 attention forward, head dim 128 (``out = softmax(q k^T) v`` in base 2 with the E8M0 1x32 scales).
+
+    q        [B, S, H, 128]   fp8 e4m3 (uint8 or float8_e4m3fn)   k, v [B, SK, HK, 128] (H = gqa HK, gqa a power of two <= 16)
+    q_scale  [B, S, H, 4]     E8M0 bytes          k_scale [B, SK, HK, 4]; both need the zeroed slack tail of the
+                                                   kernel contract (512 H 4 / 640 H 4 bytes behind the tensor)
+    v_scale  f32 V descale in a buffer of at least 4096 bytes
+    out      [B, S, H, 128]   bf16
+    path: "auto" | "vs128" | "t128" | "kvsplit" (``splits`` in {2, 4, 8}). Returns (path, splits).
+    Extensions (not in the reference): ``lse`` [B, H, S] f32 receives the natural-log LSE (vs128 / t128);
+    ``causal`` applies the bottom-right causal mask (key t visible to query i iff t <= i + SK - S).
+    """
+    B, S, H, d = q.shape
+    _, SK, HK, _ = k.shape
+    if d != D or k.shape[3] != D or H % HK or (H // HK) & (H // HK - 1) or H // HK > 16:
+        raise ValueError(f"fmha_fwd_mxfp8: head dim must be 128 and H a power-of-two multiple (<= 16) of HK (q {tuple(q.shape)}, k {tuple(k.shape)})")
+    _expect(q, "q", (B, S, H, D), 1)
+    _expect(k, "k", (B, SK, HK, D), 1)
+    _expect(v, "v", (B, SK, HK, D), 1)
+    _expect(q_scale, "q_scale", (B, S, H, 4), 1, align=4)
+    _expect(k_scale, "k_scale", (B, SK, HK, 4), 1, align=4)
+    _expect(out, "out", (B, S, H, D), 2)
+    if _cap(v_scale) < 4:
+        raise ValueError("v_scale: needs at least one f32")
+    if lse is not None:
+        _expect(lse, "lse", (B, H, S), 4)
+    if path == "auto":
+        path_id, nsplit = -1, 0
+    elif path in ("vs128", "t128"):
+        path_id, nsplit = lib.PATH_IDS[path], 0
+    elif path == "kvsplit":
+        path_id, nsplit = lib.PATH_KVSPLIT, splits or 4
+        if nsplit not in (2, 4, 8):
+            raise ValueError(f"fmha_fwd_mxfp8: unknown path {path!r} / splits {splits}")
+    else:
+        raise ValueError(f"fmha_fwd_mxfp8: unknown path {path!r} / splits {splits}")
+    dev = q.device
+    st = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
+    p = lib.Params()
+    p.o, p.q, p.k, p.v = out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr()
+    p.q_descale, p.k_descale, p.v_descale = q_scale.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr()
+    p.lse = lse.data_ptr() if lse is not None else None
+    p.bytes_q, p.bytes_k, p.bytes_v, p.bytes_o = _cap(q), _cap(k), _cap(v), _cap(out)
+    p.bytes_q_descale, p.bytes_k_descale, p.bytes_v_descale = _cap(q_scale), _cap(k_scale), _cap(v_scale)
+    p.B, p.H, p.HK, p.S, p.SK = B, H, HK, S, SK
+    p.path, p.splits, p.causal = path_id, nsplit, int(bool(causal))
+    # the workspace only matters for the KV split; size it for the split the dispatch will choose
+    want_path, want_splits = (select_path(B, H, S, SK) if path_id < 0 else (path, nsplit))
+    ws, ws_bytes = None, 0
+    if want_path == "kvsplit" and not causal:
+        ws_bytes = lib.workspace_bytes(B, H, S, want_splits)
+        ws = _ws(dev, st, ws_bytes).data_ptr()
+    with torch.cuda.device(dev):
+        return lib.run_auto(p, ws, ws_bytes, st)
+
+
+def alloc_scales(B, rows, H, device, fill=0):
+    """An E8M0 scale tensor [B, rows, H, 4] viewed from an allocation with the zeroed slack tail of the kernel
+    contract (512 H 4 bytes behind Q scales, 640 H 4 behind K scales: the larger is used for both)."""
+    base = torch.zeros(B * rows * H * 4 + 640 * H * 4, dtype=torch.uint8, device=device)
+    view = base[: B * rows * H * 4].view(B, rows, H, 4)
+    if fill:
+        view.fill_(fill)
+    return view
+
+
+def quantize_mxfp8(x, scale_out, mul=1.0):
+    """Quantise fp32 rows x[..., 128] to MXFP8 as the reference's generator does (ref_host.cpp:239-251): per 32-element
+    block E8M0 = clamp(floor(log2 amax) - 8 + 127, 0, 254), elements e4m3 round-to-nearest-even saturating at 448.
+    Writes the scales into ``scale_out`` (same leading shape, last dim 4) and returns the e4m3 bytes (uint8)."""
+    xb = (x.float() * mul).reshape(*x.shape[:-1], 4, 32)
+    amax = xb.abs().amax(dim=-1)
+    e = torch.where(amax > 0, torch.floor(torch.log2(amax)) - 8, torch.full_like(amax, -127.0))
+    eb = torch.clamp(e + 127, 0, 254)
+    scale_out.copy_(eb.to(torch.uint8))
+    y = xb * torch.exp2(-(eb - 127)).unsqueeze(-1)
+    y = torch.clamp(y, -448.0, 448.0)
+    return y.to(torch.float8_e4m3fn).view(torch.uint8).reshape(x.shape)
+
+
+def random_inputs(B, H, S, SK, HK=None, device="cuda", seed=0):
+    """Synthetic MXFP8 inputs with the distribution of the reference's REF_DATA=normal generator
+    (N(0,1) Q/K/V, Q x log2(e)/sqrt(128), per-32 E8M0 along head_dim, V e4m3 with one f32 descale),
+    drawn on the device with torch's generator. Returns (q, k, v, q_scale, k_scale, v_scale)."""
+    HK = HK or H
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    qs = alloc_scales(B, S, H, device)
+    ks = alloc_scales(B, SK, HK, device)
+    q = quantize_mxfp8(torch.randn(B, S, H, D, generator=g, device=device), qs, mul=1.4426950408889634 / math.sqrt(D))
+    k = quantize_mxfp8(torch.randn(B, SK, HK, D, generator=g, device=device), ks)
+    vv = torch.randn(B, SK, HK, D, generator=g, device=device)
+    vd = (vv.abs().amax() / 448.0).float()
+    v = torch.clamp(vv / vd, -448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+    vs = torch.zeros(1024, dtype=torch.float32, device=device)
+    vs[0] = vd
+    return q, k, v, qs, ks, vs

@@ -13,7 +13,7 @@
  *   fmha_fwd_hd128_mxfp8_v3_kvsplit_combine8h (tests/gpu/ref_host.cpp:75)
  * and read a by-value kernarg segment with the byte layout of the structs
  * below, so a launcher written against the reference's generated headers
- * (tests/gpu/generated/*_abi.h) launches them unchanged.
+ * (tests/gpu/generated/, one _abi.h per kernel) launches them unchanged.
  *
  * Numerics (all four kernels): softmax base 2 of dequant(Q).dequant(K)^T with
  * the caller folding log2(e)/sqrt(128) into Q before quantisation

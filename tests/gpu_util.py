@@ -1,0 +1,47 @@
+"""Helpers of the GPU parity tests: upload the oracle's seeded inputs and run the op through the C ABI."""
+import numpy as np
+import torch
+
+import oracle
+from amdgpu_rustdsl_amd import ops
+
+D = 128
+
+
+def upload(inp, device):
+    """Device tensors of an oracle.Inputs (descale tensors viewed from allocations with the zeroed slack)."""
+    B, H, HK, S, SK = inp.B, inp.H, inp.HK, inp.S, inp.SK
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    q = t(inp.q).view(B, S, H, D)
+    k = t(inp.k).view(B, SK, HK, D)
+    v = t(inp.v).view(B, SK, HK, D)
+    qs_all = t(inp.qs)
+    ks_all = t(inp.ks)
+    qs = qs_all[: B * S * H * 4].view(B, S, H, 4)
+    ks = ks_all[: B * SK * HK * 4].view(B, SK, HK, 4)
+    vs = t(inp.vd_buf)
+    return q, k, v, qs, ks, vs
+
+
+def run(inp, device, path="auto", splits=None, lse=False, poison=True):
+    """Runs the op; returns (bf16 output as uint16 numpy [B*S*H*128], (path, splits), lse tensor or None)."""
+    q, k, v, qs, ks, vs = upload(inp, device)
+    out = torch.empty(inp.B, inp.S, inp.H, D, dtype=torch.bfloat16, device=device)
+    if poison:
+        out.view(torch.int16).fill_(0x7fc1)   # NaN: every element must be written
+    lse_t = torch.full((inp.B, inp.H, inp.S), float("nan"), dtype=torch.float32, device=device) if lse else None
+    used = ops.fmha_fwd_mxfp8(q, k, v, qs, ks, vs, out, path=path, splits=splits, lse=lse_t, causal=inp.causal)
+    torch.cuda.synchronize()
+    o = out.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    return o, used, lse_t
+
+
+def compare_to_emulation(out, emu, inp, rows):
+    """Element statistics of the GPU output against the recipe emulation on the first `rows` rows of every (b,h)."""
+    o = out.reshape(inp.B, inp.S, inp.H, D)[:, :rows]
+    e = emu.reshape(inp.B, inp.S, inp.H, D)[:, :rows]
+    of = oracle.bf16_to_f32(o).astype(np.float64)
+    ef = oracle.bf16_to_f32(e).astype(np.float64)
+    diff = np.abs(of - ef)
+    return {"exact": float(np.mean(o == e)), "max_abs": float(np.nanmax(diff)) if diff.size else 0.0,
+            "mean_abs": float(np.mean(diff)), "nan": int(np.isnan(of).sum())}
