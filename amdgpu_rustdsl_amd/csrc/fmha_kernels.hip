@@ -43,10 +43,12 @@ namespace {
 constexpr int kD = 128;
 constexpr int kTile = 128;                    // keys per KV tile
 constexpr int kTileBytes = kTile * kD;        // 16 KiB
-constexpr int kLdsK = 0;                      // 2 slots
-constexpr int kLdsV = 2 * kTileBytes;         // 2 slots
-constexpr int kLdsKs = 4 * kTileBytes;        // 2 slots x 512 B
-constexpr int kLdsBytes = 4 * kTileBytes + 2 * 512;
+constexpr int kSlots = 3;                     // ring depth (prefetch distance 2)
+constexpr int kLdsK = 0;                      // kSlots K tiles
+constexpr int kLdsV = kSlots * kTileBytes;    // kSlots V tiles
+constexpr int kLdsQ = 2 * kSlots * kTileBytes;    // the block's Q rows (up to 256 x 128 B), swizzled like K
+constexpr int kLdsKs = kLdsQ + 256 * kD;          // kSlots x 512 B of K scales
+constexpr int kLdsBytes = kLdsKs + kSlots * 512;
 
 struct Prm {
     const uint8_t* q;
@@ -76,8 +78,11 @@ __device__ inline Prm prm_from(const fmha_mxfp8_args& a) {
     return p;
 }
 
-// LDS chunk swizzle: injective on any 8 consecutive rows and on {r..r+3, r+8..r+11} (r % 4 == 0).
-__device__ inline uint32_t swz(uint32_t r) { return (r & 3u) | ((((r >> 2) ^ (r >> 3)) & 1u) << 2); }
+// LDS chunk swizzle: 16-byte chunk c of tile row r sits at chunk c ^ swz(r), swz(r) = (r2, r1, r3) as bits 0..2.
+// Bank-conflict free (measured with SQ_LDS_BANK_CONFLICT on gfx950) for both readers: the K ds_read_b128 (lanes =
+// 32 consecutive rows, one chunk; needs bits r1, r2, r3 to map to independent chunk bits) and the transposing V
+// reads (rows {0-3, 8-11} (+4) with two chunks; needs r1, r3 independent in chunk bits 1-2).
+__device__ inline uint32_t swz(uint32_t r) { return ((r >> 2) & 1u) | (r & 2u) | (((r >> 3) & 1u) << 2); }
 
 __device__ inline uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
@@ -86,98 +91,126 @@ __device__ inline uint32_t f2h(float f) { return (uint32_t)__builtin_bit_cast(un
 
 __device__ inline float bias_of(uint32_t w) { return (h2f(w) + h2f(w >> 16)) * 4.0f; }
 
-__device__ inline void dma16(const void* src, uint32_t lds_off) {
-    __builtin_amdgcn_global_load_lds(src, (LDS_AS void*)(uintptr_t)lds_off, 16, 0, 0);
-}
-__device__ inline void dma4(const void* src, uint32_t lds_off) {
-    __builtin_amdgcn_global_load_lds(src, (LDS_AS void*)(uintptr_t)lds_off, 4, 0, 0);
+// LDS byte offset of ring slot `slot` of the region at `region`, as an opaque wave-uniform value: loop strength
+// reduction cannot see through readfirstlane, so it does not turn every (slot base + per-lane offset) address
+// into its own induction variable (one VGPR each, which spilled).
+__device__ inline uint32_t slot_base(uint32_t lds, uint32_t region, uint32_t slot, uint32_t slot_bytes) {
+    return __builtin_amdgcn_readfirstlane(lds + region + slot * slot_bytes);
 }
 
 __device__ inline v4i lds_read16(uint32_t off) { return *(const LDS_AS v4i*)(uintptr_t)off; }
 __device__ inline uint32_t lds_read4(uint32_t off) { return *(const LDS_AS uint32_t*)(uintptr_t)off; }
 
+__device__ inline v2i lds_read_tr8(uint32_t off) { return __builtin_amdgcn_ds_read_tr8_b64_v2i32((LDS_AS v2i*)(uintptr_t)off); }
+
 __device__ inline v8i cat8(v4i a, v4i b) { return (v8i){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}; }
 
+// Buffer resource over [base, base + bytes): the staging loads are range-checked by the hardware (an
+// out-of-range lane reads zeros) on top of the explicit key clamp of the last tile. The base and size are
+// wave-uniform by construction; readfirstlane states it so the resource lives in SGPRs (a resource the compiler
+// cannot prove uniform costs a waterfall loop per load).
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a), hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    void* ub = (void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(ub, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+__device__ inline void lds_write16(uint32_t off, v4i v) { *(LDS_AS v4i*)(uintptr_t)off = v; }
+__device__ inline void lds_write4(uint32_t off, uint32_t v) { *(LDS_AS uint32_t*)(uintptr_t)off = v; }
+
+// Register-staged copy of one 128-key tile (K and V: 16 KiB each; K scales: 512 B) from HBM into an LDS ring
+// slot: load() issues the buffer loads into VGPRs, store() writes them (after the slot is free) with ds_write_b128.
+// Thread tid moves 16-byte chunk (tid & 7) of rows i NT/8 + tid/8, i < kN: each 8-thread group reads one
+// contiguous 128-byte row. The chunk lands at (chunk ^ swz(row)); NT/8 is a multiple of 16, so the swizzle and
+// the per-thread offsets are the same for every i and the tile's first key rides in the scalar offset.
+// (Staging through VGPRs instead of buffer_load ... lds keeps every LDS read free of the compiler's
+// conservative vmcnt(0) before reads that might alias an in-flight LDS DMA.)
 template <int NT>
 struct Stager {
-    // global -> LDS staging of one 128-key tile: K and V (16 KiB each, 16 B per lane-instruction) and the
-    // K scales (512 B: every wave loads 64 keys' dwords, waves w and w+2 the same ones, so the vmcnt
-    // accounting is identical in every wave).
-    static constexpr int kN = kTileBytes / (NT * 16);   // instructions per thread per 16 KiB tile
-    const uint8_t* kb;   // K of this (batch, kv head)
-    const uint8_t* vb;
-    const uint8_t* ksb;
-    uint32_t k_seq, ks_row, kv_last;
-    uint32_t wave, lane;
-    uint32_t lds;   // LDS base of the ring
+    static constexpr int kN = kTileBytes / (NT * 16);   // 16-byte chunks per thread per 16 KiB tile
+    __amdgpu_buffer_rsrc_t rk, rv, rks;
+    uint32_t voff;     // (tid / 8) k_seq + 16 (tid & 7)
+    uint32_t woff;     // (tid / 8) 128 + 16 ((tid & 7) ^ swz(tid / 8))
+    uint32_t tid, k_seq, ks_row, SK, lds;
+    v4i kr[kN], vr[kN];
+    uint32_t ksr;
 
-    __device__ void stage(uint32_t key0, uint32_t slot) const {
-        {
-            const uint32_t key = min(key0 + (wave & 1u) * 64u + lane, kv_last);
-            dma4(ksb + (size_t)key * ks_row, lds + kLdsKs + slot * 512u + (wave & 1u) * 256u);
-        }
+    __device__ void init(const uint8_t* kb, const uint8_t* vb, const uint8_t* ksb, uint32_t kv_bytes, uint32_t ks_bytes,
+                         uint32_t k_seq_, uint32_t SK_, uint32_t lds_) {
+        rk = make_rsrc(kb, kv_bytes);
+        rv = make_rsrc(vb, kv_bytes);
+        rks = make_rsrc(ksb, ks_bytes);
+        tid = threadIdx.x;
+        k_seq = k_seq_;
+        ks_row = k_seq_ >> 5;
+        SK = SK_;
+        lds = lds_;
+        const uint32_t row = tid >> 3, c = tid & 7u;
+        voff = row * k_seq + (c << 4);
+        woff = row * 128u + ((c ^ swz(row)) << 4);
+    }
+
+    __device__ __forceinline__ void load(uint32_t key0) {
+        if (key0 + (uint32_t)kTile <= SK) {
 #pragma unroll
-        for (int i = 0; i < kN; ++i) {
-            const uint32_t base = (uint32_t)(i * NT) * 16u + wave * 1024u;   // wave-uniform LDS offset
-            const uint32_t p = base + lane * 16u;
-            const uint32_t row = p >> 7, pch = (p >> 4) & 7u;
-            const uint32_t key = min(key0 + row, kv_last);
-            const size_t g = (size_t)key * k_seq + ((pch ^ swz(row)) << 4);
-            dma16(kb + g, lds + kLdsK + slot * kTileBytes + base);
-            dma16(vb + g, lds + kLdsV + slot * kTileBytes + base);
+            for (int i = 0; i < kN; ++i) {
+                const uint32_t so = (key0 + (uint32_t)(i * NT / 8)) * k_seq;
+                kr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rk, voff, so, 0));
+                vr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, so, 0));
+            }
+            if (tid < 128u) ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, tid * ks_row, key0 * ks_row, 0);
+        } else {
+            // the last, partial tile: rows past the sequence end re-read the last key (masked in the softmax)
+#pragma unroll
+            for (int i = 0; i < kN; ++i) {
+                const uint32_t key = min(key0 + (uint32_t)(i * NT / 8) + (tid >> 3), SK - 1u);
+                const uint32_t off = key * k_seq + ((tid & 7u) << 4);
+                kr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+                vr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+            }
+            if (tid < 128u) ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, min(key0 + tid, SK - 1u) * ks_row, 0, 0);
         }
     }
-    static constexpr int kLoadsPerStage = 2 * kN + 1;
+
+    __device__ __forceinline__ void store(uint32_t slot) const {
+        const uint32_t kb = slot_base(lds, kLdsK, slot, kTileBytes) + woff, vb = slot_base(lds, kLdsV, slot, kTileBytes) + woff;
+#pragma unroll
+        for (int i = 0; i < kN; ++i) {
+            lds_write16(kb + i * NT * 16, kr[i]);
+            lds_write16(vb + i * NT * 16, vr[i]);
+        }
+        if (tid < 128u) lds_write4(slot_base(lds, kLdsKs, slot, 512u) + tid * 4u, ksr);
+    }
 };
 
-// Workgroup barrier that is also a compiler memory barrier (no LDS access moves across it) but, unlike
-// __syncthreads, does not drain vmcnt: the next tile's LDS DMA stays in flight across it.
-__device__ inline void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-template <int N>
-__device__ inline void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
+// Workgroup barrier that is also a compiler memory barrier (no LDS access moves across it): drains this wave's
+// LDS operations (its tile writes become visible) but, unlike __syncthreads, not vmcnt: the staging loads of a
+// later tile stay in flight across it.
+__device__ inline void block_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Softmax recipe constants (softmax.rs:24-27 exact copy; softmax.rs:80-88 lazy copy).
 struct Recipe {
     float thr, b131, conv;
 };
 
-// V^T fragment of one PV MFMA: four transposing reads 16 keys apart (2048 B). Issued as one asm block that
-// drains lgkmcnt: the compiler's ds_read_tr intrinsic is made to wait for every outstanding LDS DMA (vmcnt(0)),
-// which would serialise the next tile's staging with this tile's compute.
-__device__ inline v8i lds_read_vt(uint32_t addr) {
-    v2i r0, r1, r2, r3;
-    asm volatile(
-        "ds_read_b64_tr_b8 %0, %4\n\t"
-        "ds_read_b64_tr_b8 %1, %4 offset:2048\n\t"
-        "ds_read_b64_tr_b8 %2, %4 offset:4096\n\t"
-        "ds_read_b64_tr_b8 %3, %4 offset:6144\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
-        : "v"(addr));
-    return (v8i){r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
-}
-
-// One tile's softmax on the S^T accumulators of a wave: row max (+ partner lane), the rebase decision and
-// rescale, and the fp8 P words.
-template <bool LUT>
-__device__ __forceinline__ void softmax_tile(const Recipe& rc, v16f (&s)[4], v16f (&o)[4], v4f& lacc, v16f& bias, uint32_t& bw,
-                                             uint32_t (&pw)[4][4]) {
+// Row max of one tile's S^T accumulators: the lane's 64 values (v_max3 chain), then the partner lane l ^ 32
+// (the other key half of the same query column) through v_permlane32_swap.
+__device__ __forceinline__ float row_max(const v16f (&s)[4]) {
     float m = -1.0e30f;
 #pragma unroll
     for (int t4 = 0; t4 < 4; ++t4)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            m = fmaxf(m, s[t4][i]);
-        }
-    {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m), false, false);
-        m = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
-    }
-    // rebase decision (softmax.rs:125-160 eager: thr < m; softmax.rs:186-241 lazy: !(thr >= m), which also takes NaN)
+        for (int i = 0; i < 16; ++i) m = fmaxf(m, s[t4][i]);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m), false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
+}
+
+// The rebase decision of one tile given its row max m: when any lane's max passes the threshold, the new two-word
+// reference and the rescale of S, O and the row sums (lanes below the threshold keep their reference, delta = 0).
+template <bool LUT>
+__device__ __forceinline__ void rebase(const Recipe& rc, float m, v16f (&s)[4], v16f (&o)[4], v4f& lacc, float& bias, uint32_t& bw) {
+    // softmax.rs:125-160 eager: thr < m; softmax.rs:186-241 lazy: !(thr >= m), which also takes NaN
     const bool grow = LUT ? (rc.thr < m) : !(rc.thr >= m);
     if (__builtin_amdgcn_ballot_w64(grow)) {
         const float hi_o = h2f(bw), lo_o = h2f(bw >> 16);
@@ -204,231 +237,407 @@ __device__ __forceinline__ void softmax_tile(const Recipe& rc, v16f (&s)[4], v16
             for (int i = 0; i < 16; ++i) o[dc][i] *= corr;
 #pragma unroll
         for (int i = 0; i < 4; ++i) lacc[i] *= corr;
-        const float bnew = bias_of(bw);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) bias[i] = bnew;
+        bias = bias_of(bw);
     }
-    // P = e4m3(pknorm(S') [- LUT] / scale), 4 keys per word
-#pragma unroll
-    for (int t4 = 0; t4 < 4; ++t4)
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-            float x[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) x[c] = s[t4][4 * a + c];
-            v2u16 u01 = __builtin_bit_cast(v2u16, __builtin_amdgcn_cvt_pknorm_u16(x[0], x[1]));
-            v2u16 u23 = __builtin_bit_cast(v2u16, __builtin_amdgcn_cvt_pknorm_u16(x[2], x[3]));
-            if (LUT) {
-                // u -= LUT[(u >> 4) & 7], LUT = {0, 6, 9, 11, 11, 10, 7, 3} (reduce.rs:84-91)
-                const uint32_t i01 = (__builtin_bit_cast(uint32_t, u01) >> 4) & 0x00070007u;
-                const uint32_t i23 = (__builtin_bit_cast(uint32_t, u23) >> 4) & 0x00070007u;
-                u01 = u01 - __builtin_bit_cast(v2u16, __builtin_amdgcn_perm(0x03070a0bu, 0x0b090600u, i01));
-                u23 = u23 - __builtin_bit_cast(v2u16, __builtin_amdgcn_perm(0x03070a0bu, 0x0b090600u, i23));
-            }
-            v2s w = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16((v2s){0, 0}, __builtin_bit_cast(v2bf, u01), rc.conv, false);
-            w = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(w, __builtin_bit_cast(v2bf, u23), rc.conv, true);
-            pw[t4][a] = __builtin_bit_cast(uint32_t, w);
-        }
 }
 
-// The per-wave attention state over one key range [key_lo, key_hi) of one block.
-template <int NT, bool LUT, bool SPLIT>
-__device__ void attend(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split, uint32_t key_lo,
-                       uint32_t key_hi) {
-    constexpr int ROWS = NT / 64 * 32;
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = wave_id();
-    const uint32_t n = lane & 31u, hh = lane >> 5;
+// P = e4m3(pknorm(S') [- LUT] / scale) for one 32-key accumulator: 4 words of 4 keys.
+template <bool LUT>
+__device__ __forceinline__ void convert_p(const Recipe& rc, const v16f& s, uint32_t (&pw)[4]) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        v2u16 u01 = __builtin_bit_cast(v2u16, __builtin_amdgcn_cvt_pknorm_u16(s[4 * a], s[4 * a + 1]));
+        v2u16 u23 = __builtin_bit_cast(v2u16, __builtin_amdgcn_cvt_pknorm_u16(s[4 * a + 2], s[4 * a + 3]));
+        if (LUT) {
+            // u -= LUT[(u >> 4) & 7], LUT = {0, 6, 9, 11, 11, 10, 7, 3} (reduce.rs:84-91)
+            const uint32_t i01 = (__builtin_bit_cast(uint32_t, u01) >> 4) & 0x00070007u;
+            const uint32_t i23 = (__builtin_bit_cast(uint32_t, u23) >> 4) & 0x00070007u;
+            u01 = u01 - __builtin_bit_cast(v2u16, __builtin_amdgcn_perm(0x03070a0bu, 0x0b090600u, i01));
+            u23 = u23 - __builtin_bit_cast(v2u16, __builtin_amdgcn_perm(0x03070a0bu, 0x0b090600u, i23));
+        }
+        v2s w = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16((v2s){0, 0}, __builtin_bit_cast(v2bf, u01), rc.conv, false);
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(w, __builtin_bit_cast(v2bf, u23), rc.conv, true);
+        pw[a] = __builtin_bit_cast(uint32_t, w);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// One wave's attention over the key range [key_lo, key_hi) of its block: 32 query rows, S^T / O^T in the C layout
+// of the 32x32 MFMA (lane = query column n, half hh; value i of accumulator t4 = key 32 t4 + 8 (i / 4) + 4 hh + i % 4).
+// ---------------------------------------------------------------------------------------------------------------
+template <int NT>
+struct Wave {
+    static constexpr int ROWS = NT / 64 * 32;
+    uint32_t lane, wave, n, hh, lds;
+    uint32_t row0;
+    int sq[2];
+    float vd;
+    uint32_t kfo;      // K / Q fragment offset in a tile: row n, chunk (hh ^ swz(n)); chunk 4c + 2e + hh = kfo ^ (4c + 2e) << 4
+    uint32_t vfo;      // V^T read offset: row rlo, chunk ((g & 1) ^ swz(rlo)), half pp; dim group dc = vfo ^ (2 dc) << 4
+    uint32_t onew;
+    // causal limits: query row i sees keys [0, i + SK - S + 1) (cut to [.., key_hi))
+    uint32_t lim_row, lim_wave_min, lim_wave_max, key_hi;
+    // softmax state
+    uint32_t bw;       // two f16 words (hi = low half); b = 64 makes tile 0 rebase
+    float bias;        // b of this lane's query: the seed of every S accumulator
+    v16f o[4];
+    v4f lacc;
+
+    // Q rows of this wave -> LDS (swizzled like a K tile, at kLdsQ + 4096 wave): the QK MFMAs read their B operand
+    // from there one k-half at a time, so only 8 Q VGPRs are live at the phase's register peak.
+    __device__ __forceinline__ void init(const Prm& p, uint32_t lds_, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_hi_) {
+        lane = threadIdx.x & 63u;
+        wave = wave_id();
+        n = lane & 31u;
+        hh = lane >> 5;
+        lds = lds_;
+        key_hi = key_hi_;
+        row0 = qtile * ROWS + wave * 32u;
+        const uint32_t row = row0 + n;
+        const uint32_t row_c = min(row, p.S - 1u);
+        kfo = n * 128u + ((hh ^ swz(n)) << 4);
+        {
+            const uint8_t* qrow = p.q + (size_t)bidx * p.q_b + (size_t)row_c * p.q_seq + head * kD;
+            const uint32_t qb = lds + kLdsQ + wave * 4096u;
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    lds_write16(qb + (kfo ^ ((uint32_t)(4 * c + 2 * e) << 4)), *(const v4i*)(qrow + 64 * c + 32 * e + 16 * hh));
+        }
+        const uint32_t qsw = *(const uint32_t*)(p.qs + (size_t)bidx * p.qs_b + (size_t)row_c * (p.H * 4u) + head * 4u);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) sq[c] = (int)(((qsw >> (8 * (2 * c + hh))) - 9u) & 0xffu);
+        vd = *p.vd;
+        lim_row = lim_wave_min = lim_wave_max = key_hi;
+        if (p.flags & 1u) {
+            const int off = (int)p.SK - (int)p.S + 1;
+            lim_row = (uint32_t)max(0, min((int)key_hi, (int)row + off));
+            lim_wave_min = (uint32_t)max(0, min((int)key_hi, (int)row0 + off));
+            lim_wave_max = (uint32_t)max(0, min((int)key_hi, (int)row0 + 31 + off));
+        }
+        {
+            // ds_read_b64_tr_b8 source lane (g, jj, pp) reads key 16 r + rlo of the 64-key half, dims
+            // 32 dc + 16 (g & 1) + 8 pp .. +7
+            const uint32_t g = lane >> 4, jj = (lane >> 1) & 7u, pp = lane & 1u;
+            const uint32_t rlo = 8u * (jj >> 2) + 4u * (g >> 1) + (jj & 3u);
+            vfo = rlo * 128u + (((g & 1u) ^ swz(rlo)) << 4) + 8u * pp;
+        }
+        // ones pattern of the row-sum MFMA (16x16x128): lane la holds A row la % 16, k-groups la / 16; row m sums
+        // the P bytes of query (m % 2 ? n + 16 : n) -> ones iff (la / 16) % 2 == la % 2
+        onew = (((lane >> 4) & 1u) == (lane & 1u)) ? 0x38383838u : 0u;
+        bw = 0x48004800u;
+        bias = bias_of(bw);
+#pragma unroll
+        for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[dc][i] = 0.0f;
+        lacc = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    __device__ __forceinline__ bool active(uint32_t key0) const { return key0 < lim_wave_max; }
+    __device__ __forceinline__ bool needs_mask(uint32_t key0) const { return key0 + kTile > min(key_hi, lim_wave_min); }
+    // keys at or past the range end / causal limit: -1e30 takes no part in the max and converts to P = 0 (pknorm
+    // clamps), the reference's two fills (reduce.rs:13-49) in one
+    __device__ __forceinline__ void apply_mask(v16f (&s)[4], uint32_t key0) const {
+        const int nvalid = (int)min(key_hi, lim_row) - (int)key0 - 4 * (int)hh;
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[t4][i] = (32 * t4 + 8 * (i >> 2) + (i & 3)) < nvalid ? s[t4][i] : -1.0e30f;
+    }
+
+    // 32-byte K or Q fragment of k-half c (c = 0: d 0..63, 1: d 64..127) of row n of the tile at `base`
+    __device__ __forceinline__ v8i frag(uint32_t base, int c) const {
+        return cat8(lds_read16(base + (kfo ^ ((uint32_t)(4 * c) << 4))), lds_read16(base + (kfo ^ ((uint32_t)(4 * c + 2) << 4))));
+    }
+    __device__ __forceinline__ v8i qfrag(int c) const { return frag(lds + kLdsQ + wave * 4096u, c); }
+    // K-scale word of 32-key block t4, shifted so op_sel byte 2c is the lane half's E8M0 byte 2c + hh
+    __device__ __forceinline__ uint32_t kscale(uint32_t ksb, int t4) const { return lds_read4(ksb + (32u * t4 + n) * 4u) >> (8u * hh); }
+    // V^T fragment of PV MFMA (j, dc): four transposing reads 16 keys apart
+    __device__ __forceinline__ v8i vfrag(uint32_t vb, int j, int dc) const {
+        const uint32_t va = vb + 8192u * j + (vfo ^ ((uint32_t)(2 * dc) << 4));
+        const v2i r0 = lds_read_tr8(va), r1 = lds_read_tr8(va + 2048u), r2 = lds_read_tr8(va + 4096u), r3 = lds_read_tr8(va + 6144u);
+        return (v8i){r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+    }
+    __device__ __forceinline__ static v8i pfrag(const uint32_t (&pw)[4][4], int j) {
+        return (v8i){(int)pw[2 * j][0], (int)pw[2 * j][1], (int)pw[2 * j][2], (int)pw[2 * j][3],
+                     (int)pw[2 * j + 1][0], (int)pw[2 * j + 1][1], (int)pw[2 * j + 1][2], (int)pw[2 * j + 1][3]};
+    }
+    // The ones operand of the row-sum MFMA, rebuilt where it is used (an opaque copy, so the compiler neither keeps
+    // it live across the loop nor hoists it: 8 VGPRs only around the row-sum MFMAs).
+    __device__ __forceinline__ v8i ones_op() const {
+        uint32_t x;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(x) : "v"(onew));
+        return (v8i){(int)x, (int)x, (int)x, (int)x, (int)x, (int)x, (int)x, (int)x};
+    }
+    __device__ __forceinline__ v16f qk_mfma(const v8i& kf, const v8i& qf, const v16f& c_in, uint32_t ksw, int c) const {
+        // scaled fp8 MFMA: A = K (rows = keys), B = Q^T (columns = queries), E8M0 scales per 32 of k
+        return c == 0 ? __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf, qf, c_in, 0, 0, 0, (int)ksw, 0, sq[0])
+                      : __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf, qf, c_in, 0, 0, 2, (int)ksw, 0, sq[1]);
+    }
+
+    // PV of one tile: O^T += V^T P^T (8 MFMAs) and the row sums of P (2 MFMAs). Each V^T fragment is read one MFMA
+    // ahead; a scheduling fence after every MFMA keeps the compiler from hoisting the phase's 32 reads to its top.
+    __device__ __forceinline__ void pv_all(uint32_t slot, const uint32_t (&pw)[4][4]) {
+        const uint32_t vb = slot_base(lds, kLdsV, slot, kTileBytes);
+        v8i vf = vfrag(vb, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const int j = g >> 2, dc = g & 3;
+            const v8i pf = pfrag(pw, j);
+            v8i vn = vf;
+            if (g < 7) vn = vfrag(vb, (g + 1) >> 2, (g + 1) & 3);
+            if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones_op(), pf, lacc, 0, 0, 0, 127, 0, 127);
+            o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, o[dc], 0, 0, 0, 127, 0, 127);
+            vf = vn;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // S(t+1): k-half 0 of all four 32-key accumulators, then k-half 1 (one Q fragment live at a time). The seed
+    // (16 copies of b) is written into s[3] and is the C input of the first MFMA of s[0..2]; s[3] then accumulates
+    // in place: no separate seed registers. One K fragment is read one MFMA ahead.
+    __device__ __forceinline__ void qk_all(uint32_t nslot, v16f (&s)[4]) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[3][i] = bias;
+        const uint32_t kb = slot_base(lds, kLdsK, nslot, kTileBytes);
+        const uint32_t ksb = slot_base(lds, kLdsKs, nslot, 512u);
+        auto kread = [&](int g) { return frag(kb + 4096u * (g & 3), g >> 2); };   // g = 4 c + t4
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const v8i qf = qfrag(c);
+            v8i kc = kread(4 * c);
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) {
+                const int g = 4 * c + t4;
+                v8i kn = kc;
+                if (g < 7) kn = kread(g + 1);
+                const uint32_t ksw = kscale(ksb, t4);
+                s[t4] = qk_mfma(kc, qf, c == 0 ? s[3] : s[t4], ksw, c);
+                kc = kn;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+};
+
+// The row sum of this lane's query (the ones pattern puts it in D dword (lane / 16) % 2).
+__device__ __forceinline__ float row_sum(const v4f& lacc, uint32_t lane) { return ((lane >> 4) & 1u) ? lacc[1] : lacc[0]; }
+
+// Epilogue. Full-sequence kernels: O = O^T . (v_descale / l) -> bf16 rows (state.rs:79-83), 8-byte stores of 4
+// dims; the optional natural-log LSE. KV split: the fp16 partial O-hat = (O / 16) (v_descale / l_total) with
+// l_total = l / 16 and lse = log2(l_total) - 2048 (hi + lo) (block3.rs:291-356, softmax.rs:308-322), partial row
+// split * rows_total + (b S + row) H + h. A row with no visible key (causal, S > SK) writes zeros.
+template <bool SPLIT, int NT>
+__device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32_t head, uint32_t bidx, uint32_t split, const Recipe& rc) {
+    // lane-derived values recomputed here from an opaque lane id: kept from the prologue they would be live (and
+    // spilled) across the whole loop
+    uint32_t lane;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+    const uint32_t hh = lane >> 5, row = w.row0 + (lane & 31u);
+    const float l = row_sum(w.lacc, lane);
+    if (row >= p.S) return;
+    const uint32_t dbase = 4u * hh;
+    if (!SPLIT) {
+        const float fin = l > 0.0f ? __builtin_amdgcn_rcpf(l) * w.vd : 0.0f;
+        // wave-uniform part of the address in SGPRs (readfirstlane), the lane's row on top
+        const uint64_t ob = (uint64_t)(uintptr_t)(p.o + (size_t)bidx * p.o_b + head * 256u);
+        // readfirstlane returns int: both words go through uint32_t, or the low word would sign-extend into the high
+        const uint32_t ob_lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)ob);
+        const uint32_t ob_hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(ob >> 32));
+        uint8_t* obase = (uint8_t*)(uintptr_t)(((uint64_t)ob_hi << 32) | (uint64_t)ob_lo);
+        uint8_t* orow = obase + (size_t)row * p.o_seq;
+#pragma unroll
+        for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const v2bf w0 = {(__bf16)(w.o[dc][4 * a] * fin), (__bf16)(w.o[dc][4 * a + 1] * fin)};
+                const v2bf w1 = {(__bf16)(w.o[dc][4 * a + 2] * fin), (__bf16)(w.o[dc][4 * a + 3] * fin)};
+                *(v2i*)(orow + (32 * dc + 8 * a + dbase) * 2) = (v2i){__builtin_bit_cast(int, w0), __builtin_bit_cast(int, w1)};
+            }
+        if (p.lse_out && hh == 0) {
+            // natural-log LSE of the scores (extension): P = 2^(S + 512 b - 127) / conv, l = sum P
+            const float hl = h2f(w.bw) + h2f(w.bw >> 16);
+            const float lse2 = l > 0.0f ? __builtin_amdgcn_logf(l) - hl * 2048.0f + 127.0f + __builtin_amdgcn_logf(rc.conv) : -INFINITY;
+            p.lse_out[((size_t)bidx * p.H + head) * p.S + row] = lse2 * 0.69314718055994531f;
+        }
+    } else {
+        const float l_total = l * 0.0625f;
+        const float fin = l > 0.0f ? __builtin_amdgcn_rcpf(l_total) * w.vd : 0.0f;
+        const size_t prow = (size_t)split * p.rows_total + ((size_t)bidx * p.S + row) * p.H + head;
+        uint8_t* orow = p.ohat + prow * 256u;
+#pragma unroll
+        for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                uint32_t wd[2];
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const uint32_t lo16 = f2h((w.o[dc][4 * a + 2 * c] * 0.0625f) * fin);
+                    const uint32_t hi16 = f2h((w.o[dc][4 * a + 2 * c + 1] * 0.0625f) * fin);
+                    wd[c] = lo16 | (hi16 << 16);
+                }
+                *(v2i*)(orow + (32 * dc + 8 * a + dbase) * 2) = (v2i){(int)wd[0], (int)wd[1]};
+            }
+        if (hh == 0) {
+            const float hl = h2f(w.bw) + h2f(w.bw >> 16);
+            // an empty range (l = 0) gets -1e30: the combine gives it weight 0
+            p.lse[prow] = l > 0.0f ? __builtin_amdgcn_logf(l_total) + (hl * 2048.0f) * -1.0f : -1.0e30f;
+        }
+    }
+}
+
+// Two 4-wave groups one phase apart (waves 0-3: A, 4-7: B; the hardware places waves w and w + 4 on one SIMD).
+// Per tile each wave runs a VALU phase V(t) (row max, rebase, P) and an MFMA phase M(t) (PV(t), then QK(t+1));
+// with B one phase behind A, one wave of every SIMD pair converts while the other multiplies, and s_setprio
+// hands the MFMA-phase wave the issue priority. Between consecutive barriers (global phase f): f = 2t: A V(t),
+// B M(t-1); f = 2t + 1: A M(t), B V(t). Tile u's slot (u % 3) is read in phases 2u-1 .. 2u+2 and must be written
+// before 2u-1: A writes its share of tile t+1 in V(t) (loaded in M(t-1)), B its share of tile t+2 in V(t)
+// (loaded in M(t-1)); every write lands in a slot whose last read phase has passed.
+template <bool LUT, bool SPLIT>
+__device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split,
+                                uint32_t key_lo, uint32_t key_hi) {
+    constexpr int NT = 512;
     const Recipe rc = LUT ? Recipe{120.0f / 512.0f, 131.0f / 512.0f, 1.0f}
                           : Recipe{__builtin_bit_cast(float, 0x3e85d086u), __builtin_bit_cast(float, 0x3e7df17eu), 0.25f};
+    Wave<NT> w;
+    w.init(p, lds, qtile, head, bidx, key_hi);
+    const bool grp_b = w.wave >= 4u;
     const uint32_t kvh = head / p.gqa;
-    const uint32_t row0 = qtile * ROWS + wave * 32u;
-    const uint32_t row = row0 + n;
-    const uint32_t row_c = min(row, p.S - 1u);
     const bool causal = (p.flags & 1u) != 0;
-
-    // ---- Q fragments (B operand of the QK MFMA, resident) and their scales
-    const uint8_t* qrow = p.q + (size_t)bidx * p.q_b + (size_t)row_c * p.q_seq + head * kD;
-    v8i qf[2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        const v4i a = *(const v4i*)(qrow + 64 * c + 16 * hh);
-        const v4i b = *(const v4i*)(qrow + 64 * c + 32 + 16 * hh);
-        qf[c] = cat8(a, b);
-    }
-    const uint32_t qsw = *(const uint32_t*)(p.qs + (size_t)bidx * p.qs_b + (size_t)row_c * (p.H * 4u) + head * 4u);
-    int sq[2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c) sq[c] = (int)(((qsw >> (8 * (2 * c + hh))) - 9u) & 0xffu);
-    const float vd = *p.vd;
-
-    // ---- causal limits: query row i sees keys [0, i + SK - S + 1)
-    uint32_t lim_row = key_hi, lim_wave_min = key_hi, lim_wave_max = key_hi, lim_blk_max = key_hi;
-    if (causal) {
-        const int off = (int)p.SK - (int)p.S + 1;
-        lim_row = (uint32_t)max(0, min((int)key_hi, (int)row + off));
-        lim_wave_min = (uint32_t)max(0, min((int)key_hi, (int)row0 + off));
-        lim_wave_max = (uint32_t)max(0, min((int)key_hi, (int)row0 + 31 + off));
-        lim_blk_max = (uint32_t)max(0, min((int)key_hi, (int)(qtile * ROWS + ROWS - 1) + off));
-    }
-    const uint32_t key_end = causal ? min(key_hi, lim_blk_max) : key_hi;   // block's last useful key + 1
+    uint32_t key_end = key_hi;   // the block's last useful key + 1
+    if (causal) key_end = (uint32_t)max(0, min((int)key_hi, (int)(qtile * Wave<NT>::ROWS + Wave<NT>::ROWS - 1) + (int)p.SK - (int)p.S + 1));
     const uint32_t ntiles = key_end > key_lo ? (key_end - key_lo + kTile - 1) / kTile : 0;
 
     Stager<NT> st;
-    st.kb = p.k + (size_t)bidx * p.k_b + kvh * kD;
-    st.vb = p.v + (size_t)bidx * p.v_b + kvh * kD;
-    st.k_seq = p.k_seq;
-    st.ks_row = p.k_seq >> 5;
-    st.ksb = p.ks + (size_t)bidx * p.ks_b + kvh * 4u;
-    st.kv_last = p.SK - 1u;
-    st.wave = wave;
-    st.lane = lane;
-    st.lds = lds;
+    st.init(p.k + (size_t)bidx * p.k_b + kvh * kD, p.v + (size_t)bidx * p.v_b + kvh * kD, p.ks + (size_t)bidx * p.ks_b + kvh * 4u,
+            (p.SK - 1u) * p.k_seq + kD, (p.SK - 1u) * (p.k_seq >> 5) + 4u, p.k_seq, p.SK, lds);
+    auto slot_of = [](uint32_t t) { return t % 3u; };
+    auto key_of = [&](uint32_t t) { return key_lo + t * kTile; };
 
-    // ---- per-lane LDS addresses
-    // K fragment (A operand, lane = key row n of the 32-key block, half hh): chunks 4c + 2e + hh of row n
-    uint32_t kaddr[2][2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) kaddr[c][e] = n * 128u + (((uint32_t)(4 * c + 2 * e) + hh) ^ swz(n)) * 16u;
-    // V^T fragment via ds_read_b64_tr_b8: source lane (g, jj, pp) reads key 16 r + rlo of the 64-key half,
-    // dims 32 dc + 16 (g & 1) + 8 pp .. +7
-    uint32_t vaddr[4];
-    {
-        const uint32_t g = lane >> 4, jj = (lane >> 1) & 7u, pp = lane & 1u;
-        const uint32_t rlo = 8u * (jj >> 2) + 4u * (g >> 1) + (jj & 3u);
-#pragma unroll
-        for (int dc = 0; dc < 4; ++dc) vaddr[dc] = rlo * 128u + ((((uint32_t)(2 * dc)) + (g & 1u)) ^ swz(rlo)) * 16u + 8u * pp;
-    }
-    // ones pattern of the row-sum MFMA (16x16x128): lane la holds A row la % 16, k-groups la / 16; row m sums
-    // the P bytes of query (m % 2 ? n + 16 : n) -> ones iff (la / 16) % 2 == la % 2
-    const int onew = (((lane >> 4) & 1u) == (lane & 1u)) ? 0x38383838 : 0;
-    const v8i ones = (v8i){onew, onew, onew, onew, onew, onew, onew, onew};
-
-    // ---- state
-    uint32_t bw = 0x48004800u;   // two f16 words (hi = low half); b = 64 makes tile 0 rebase
-    v16f bias;
-    {
-        const float b0 = bias_of(bw);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) bias[i] = b0;
-    }
-    v16f o[4];
-#pragma unroll
-    for (int dc = 0; dc < 4; ++dc)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[dc][i] = 0.0f;
-    v4f lacc = {0.0f, 0.0f, 0.0f, 0.0f};
-
-    if (ntiles > 0) st.stage(key_lo, 0);
-    for (uint32_t it = 0; it < ntiles; ++it) {
-        const uint32_t slot = it & 1u;
-        const uint32_t key0 = key_lo + it * kTile;
-        if (it + 1 < ntiles) {
-            st.stage(key0 + kTile, slot ^ 1u);
-            wait_vmcnt<Stager<NT>::kLoadsPerStage>();
-        } else {
-            wait_vmcnt<0>();
+    v16f s[4];
+    if (ntiles > 0) {
+        st.load(key_of(0));
+        st.store(0);
+        if (ntiles > 1) {
+            st.load(key_of(1));
+            if (grp_b) st.store(1);      // A keeps its share of tile 1 for V(0)
         }
+        if (grp_b && ntiles > 2) st.load(key_of(2));
         block_barrier();
-
-        const uint32_t kbase = lds + kLdsK + slot * kTileBytes;
-        const uint32_t vbase = lds + kLdsV + slot * kTileBytes;
-        const uint32_t ksbase = lds + kLdsKs + slot * 512u;
-        // keys of this tile valid for this lane: < kv end of the range, < causal limit
-        const uint32_t vlim = min(key_hi, lim_row);
-        const bool wave_skip = causal && key0 >= lim_wave_max;   // every key of the tile is past the wave's last visible key
-        if (!wave_skip) {
-            // ---- S^T = K Q^T (scaled MFMA, 2 per 32-key block), seeded with the reference b
-            v16f s[4];
-#pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) {
-                const uint32_t ksw = lds_read4(ksbase + (32u * t4 + n) * 4u) >> (8u * hh);
-                const v8i kf0 = cat8(lds_read16(kbase + 4096u * t4 + kaddr[0][0]), lds_read16(kbase + 4096u * t4 + kaddr[0][1]));
-                const v8i kf1 = cat8(lds_read16(kbase + 4096u * t4 + kaddr[1][0]), lds_read16(kbase + 4096u * t4 + kaddr[1][1]));
-                // d 0..63 then d 64..127; op_sel picks K-scale byte 2c of the lane-half-shifted word
-                s[t4] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf0, qf[0], bias, 0, 0, 0, (int)ksw, 0, sq[0]);
-                s[t4] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf1, qf[1], s[t4], 0, 0, 2, (int)ksw, 0, sq[1]);
-            }
-            // ---- softmax: row max, rebase, P (the masked form only on tiles that cross the range end / causal limit)
+        if (w.active(key_of(0))) w.qk_all(0, s);
+        if (grp_b) block_barrier();      // B starts one phase behind
+        for (uint32_t t = 0; t < ntiles; ++t) {
+            // ---- V(t)
+            __builtin_amdgcn_s_setprio(0);
+            if (!grp_b && t + 1 < ntiles) st.store(slot_of(t + 1));
+            if (grp_b && t + 2 < ntiles) st.store(slot_of(t + 2));
+            const bool act = w.active(key_of(t));
             uint32_t pw[4][4];
-            if (key0 + kTile > min(key_hi, lim_wave_min)) {
-                // keys at or past the range end / causal limit: -1e30 takes no part in the max and converts to P = 0
-                // (pknorm clamps), the reference's two fills (reduce.rs:13-49) in one
-                const int nvalid = (int)vlim - (int)key0 - 4 * (int)hh;
+            if (act) {
+                if (w.needs_mask(key_of(t))) w.apply_mask(s, key_of(t));
+                rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
 #pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i)
-                        s[t4][i] = (32 * t4 + 8 * (i >> 2) + (i & 3)) < nvalid ? s[t4][i] : -1.0e30f;
+                for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
             }
-            softmax_tile<LUT>(rc, s, o, lacc, bias, bw, pw);
-            // ---- row sums of P and O^T += V^T P^T, one 64-key half at a time
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const v8i pf = (v8i){(int)pw[2 * j][0], (int)pw[2 * j][1], (int)pw[2 * j][2], (int)pw[2 * j][3],
-                                     (int)pw[2 * j + 1][0], (int)pw[2 * j + 1][1], (int)pw[2 * j + 1][2], (int)pw[2 * j + 1][3]};
-                lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, pf, lacc, 0, 0, 0, 127, 0, 127);
-#pragma unroll
-                for (int dc = 0; dc < 4; ++dc) {
-                    const v8i vf = lds_read_vt(vbase + vaddr[dc] + 8192u * j);
-                    o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, o[dc], 0, 0, 0, 127, 0, 127);
-                }
-            }
+            block_barrier();
+            // ---- M(t): PV(t), then (P dead) the staging loads, then QK(t+1)
+            __builtin_amdgcn_s_setprio(1);
+            if (act) w.pv_all(slot_of(t), pw);
+            if (!grp_b && t + 2 < ntiles) st.load(key_of(t + 2));
+            if (grp_b && t + 3 < ntiles) st.load(key_of(t + 3));
+            if (t + 1 < ntiles && w.active(key_of(t + 1))) w.qk_all(slot_of(t + 1), s);
+            block_barrier();
+        }
+        if (!grp_b) block_barrier();     // A ends one phase ahead: the barrier counts match
+        __builtin_amdgcn_s_setprio(0);
+    }
+    epilogue<SPLIT>(p, w, head, bidx, split, rc);
+}
+
+// One 4-wave group (_t128: one wave per SIMD, so each wave overlaps its own VALU with its own MFMAs): S(t) is
+// computed and decided one iteration ahead. Iteration t: [P(t) conversion | QK(t+1)] then [PV(t) | row max of
+// S(t+1)]; the tile t+2 staged through registers lands in slot (t+2) % 3 (tile t-1's: its last read was in
+// iteration t-1), one barrier, then the rebase decision of tile t+1. The last tile runs [P | PV] alone.
+template <bool LUT>
+__device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_lo,
+                                 uint32_t key_hi) {
+    constexpr int NT = 256;
+    const Recipe rc = LUT ? Recipe{120.0f / 512.0f, 131.0f / 512.0f, 1.0f}
+                          : Recipe{__builtin_bit_cast(float, 0x3e85d086u), __builtin_bit_cast(float, 0x3e7df17eu), 0.25f};
+    Wave<NT> w;
+    w.init(p, lds, qtile, head, bidx, key_hi);
+    const uint32_t kvh = head / p.gqa;
+    const bool causal = (p.flags & 1u) != 0;
+    uint32_t key_end = key_hi;
+    if (causal) key_end = (uint32_t)max(0, min((int)key_hi, (int)(qtile * Wave<NT>::ROWS + Wave<NT>::ROWS - 1) + (int)p.SK - (int)p.S + 1));
+    const uint32_t ntiles = key_end > key_lo ? (key_end - key_lo + kTile - 1) / kTile : 0;
+    Stager<NT> st;
+    st.init(p.k + (size_t)bidx * p.k_b + kvh * kD, p.v + (size_t)bidx * p.v_b + kvh * kD, p.ks + (size_t)bidx * p.ks_b + kvh * 4u,
+            (p.SK - 1u) * p.k_seq + kD, (p.SK - 1u) * (p.k_seq >> 5) + 4u, p.k_seq, p.SK, lds);
+    auto key_of = [&](uint32_t t) { return key_lo + t * kTile; };
+
+    v16f s[4];
+    if (ntiles > 0) {
+        st.load(key_of(0));
+        st.store(0);
+        if (ntiles > 1) {
+            st.load(key_of(1));
+            st.store(1);
         }
         block_barrier();
-    }
-
-    // ---- epilogue
-    const float l = ((lane >> 4) & 1u) ? lacc[1] : lacc[0];   // the lane's query row sum (see the ones pattern)
-    if (!SPLIT) {
-        const float fin = __builtin_amdgcn_rcpf(l) * vd;   // state.rs:79-83
-        if (row < p.S) {
-            uint8_t* orow = p.o + (size_t)bidx * p.o_b + (size_t)row * p.o_seq + head * 256u;
-#pragma unroll
-            for (int dc = 0; dc < 4; ++dc)
-#pragma unroll
-                for (int a = 0; a < 4; ++a) {
-                    const v2bf w0 = {(__bf16)(o[dc][4 * a] * fin), (__bf16)(o[dc][4 * a + 1] * fin)};
-                    const v2bf w1 = {(__bf16)(o[dc][4 * a + 2] * fin), (__bf16)(o[dc][4 * a + 3] * fin)};
-                    const v2i pk = {__builtin_bit_cast(int, w0), __builtin_bit_cast(int, w1)};
-                    *(v2i*)(orow + (32 * dc + 8 * a + 4 * hh) * 2) = pk;
-                }
-            if (p.lse_out && hh == 0) {
-                // natural-log LSE of the scores (extension): P = 2^(S + 512 b - 127) / conv, l = sum P
-                const float hl = h2f(bw) + h2f(bw >> 16);
-                const float lse2 = __builtin_amdgcn_logf(l) - hl * 2048.0f + 127.0f + __builtin_amdgcn_logf(rc.conv);
-                p.lse_out[((size_t)bidx * p.H + head) * p.S + row] = lse2 * 0.69314718055994531f;
-            }
+        if (w.active(key_of(0))) {
+            w.qk_all(0, s);
+            if (w.needs_mask(key_of(0))) w.apply_mask(s, key_of(0));
+            rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
         }
-    } else {
-        // block3.rs:291-356 / softmax.rs:308-322: Ohat = (O / 16) * (v_descale / l_total), l_total = l / 16;
-        // lse = log2(l_total) - 2048 (hi + lo)
-        const float l_total = l * 0.0625f;
-        const float fin = __builtin_amdgcn_rcpf(l_total) * vd;
-        if (row < p.S) {
-            const size_t prow = (size_t)split * p.rows_total + ((size_t)bidx * p.S + row) * p.H + head;
-            uint8_t* orow = p.ohat + prow * 256u;
+        uint32_t slot = 0;
+        for (uint32_t t = 0; t + 1 < ntiles; ++t) {
+            const uint32_t nslot = slot == 2u ? 0u : slot + 1u;
+            const uint32_t sslot = nslot == 2u ? 0u : nslot + 1u;   // slot of tile t+2
+            if (t + 2 < ntiles) st.load(key_of(t + 2));
+            const bool act = w.active(key_of(t)), act_next = w.active(key_of(t + 1));
+            uint32_t pw[4][4];
+            if (act_next) {
+                // P(t) conversion interleaved with k-half 0 of QK(t+1) (accumulator t4 of S(t) is dead once
+                // converted; a separate seed, this path has the registers), then k-half 1
+                const uint32_t kb = slot_base(w.lds, kLdsK, nslot, kTileBytes), ksb = slot_base(w.lds, kLdsKs, nslot, 512u);
+                v16f seed;
 #pragma unroll
-            for (int dc = 0; dc < 4; ++dc)
+                for (int i = 0; i < 16; ++i) seed[i] = w.bias;
+                const v8i q0 = w.qfrag(0);
 #pragma unroll
-                for (int a = 0; a < 4; ++a) {
-                    uint32_t w[2];
-#pragma unroll
-                    for (int c = 0; c < 2; ++c) {
-                        const uint32_t lo16 = f2h((o[dc][4 * a + 2 * c] * 0.0625f) * fin);
-                        const uint32_t hi16 = f2h((o[dc][4 * a + 2 * c + 1] * 0.0625f) * fin);
-                        w[c] = lo16 | (hi16 << 16);
-                    }
-                    *(v2i*)(orow + (32 * dc + 8 * a + 4 * hh) * 2) = (v2i){(int)w[0], (int)w[1]};
+                for (int t4 = 0; t4 < 4; ++t4) {
+                    convert_p<LUT>(rc, s[t4], pw[t4]);
+                    s[t4] = w.qk_mfma(w.frag(kb + 4096u * t4, 0), q0, seed, w.kscale(ksb, t4), 0);
                 }
-            if (hh == 0) {
-                const float hl = h2f(bw) + h2f(bw >> 16);
-                p.lse[prow] = __builtin_amdgcn_logf(l_total) + (hl * 2048.0f) * -1.0f;
+                const v8i q1 = w.qfrag(1);
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4) s[t4] = w.qk_mfma(w.frag(kb + 4096u * t4, 1), q1, s[t4], w.kscale(ksb, t4), 1);
+            } else if (act) {
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
             }
+            if (act) w.pv_all(slot, pw);
+            float m = 0.0f;
+            if (act_next) {
+                if (w.needs_mask(key_of(t + 1))) w.apply_mask(s, key_of(t + 1));
+                m = row_max(s);
+            }
+            if (t + 2 < ntiles) st.store(sslot);
+            block_barrier();
+            if (act_next) rebase<LUT>(rc, m, s, w.o, w.lacc, w.bias, w.bw);
+            slot = nslot;
+        }
+        if (w.active(key_of(ntiles - 1))) {
+            uint32_t pw[4][4];
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
+            w.pv_all(slot, pw);
         }
     }
+    epilogue<false>(p, w, head, bidx, 0, rc);
 }
 
 // Workgroup -> (q tile, head, z): consecutive tiles of one (batch, head) land on one XCD (the hardware deals
@@ -444,10 +653,10 @@ __device__ inline void block_coords(uint32_t& qt, uint32_t& head, uint32_t& z) {
     const uint32_t nblk = gx * gy * gz;
     uint32_t L = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
     if ((nblk & 7u) == 0u) L = (L & 7u) * (nblk >> 3) + (L >> 3);
-    qt = L % gx;
+    qt = __builtin_amdgcn_readfirstlane(L % gx);
     const uint32_t rest = L / gx;
-    head = rest % gy;
-    z = rest / gy;
+    head = __builtin_amdgcn_readfirstlane(rest % gy);
+    z = __builtin_amdgcn_readfirstlane(rest / gy);
 }
 
 template <int NT>
@@ -456,8 +665,13 @@ __device__ void full_kernel(const fmha_mxfp8_args& a, uint32_t lds) {
     uint32_t qt, head, z;
     block_coords(qt, head, z);
     const bool lut = (p.SK + 127u) / 128u < 4u;   // state.rs:75-77
-    if (lut) attend<NT, true, false>(p, lds, qt, head, z, 0, 0, p.SK);
-    else attend<NT, false, false>(p, lds, qt, head, z, 0, 0, p.SK);
+    if (NT == 512) {
+        if (lut) attend_pingpong<true, false>(p, lds, qt, head, z, 0, 0, p.SK);
+        else attend_pingpong<false, false>(p, lds, qt, head, z, 0, 0, p.SK);
+    } else {
+        if (lut) attend_pipelined<true>(p, lds, qt, head, z, 0, p.SK);
+        else attend_pipelined<false>(p, lds, qt, head, z, 0, p.SK);
+    }
 }
 
 }  // namespace
@@ -496,8 +710,8 @@ extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvs
     const uint32_t tile_hi = min(ntiles, tile_lo + tps);
     const uint32_t key_lo = tile_lo * 128u, key_hi = min(tile_hi * 128u, p.SK);
     const bool lut = ntiles < 4u;
-    if (lut) attend<512, true, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
-    else attend<512, false, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+    if (lut) attend_pingpong<true, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+    else attend_pingpong<false, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
 }
 
 // epilogue.rs:89-167 / io.rs:164-185: thread t -> 8 consecutive outputs of row t >> 4 (tail threads redo the last group)

@@ -1,0 +1,205 @@
+"""Benchmark of the MXFP8 FMHA forward (hd128) on one MI355X: the reference's headline metric.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg5|cfg1] [--no-cpu]
+
+One step = one call of fmha_fwd_hd128_mxfp8_auto (dispatch + validate + launch, plus the combine on the KV-split
+path) on inputs already resident in HBM. Prints ONE JSON line. TFLOP/s = 4 B H S SK 128 / t (algorithmic,
+non-causal count, tests/gpu/ref_host.cpp:403); the causal workload counts the visible pairs.
+
+roofline: the dominant kernel's algorithmic FLOP per launch / its average duration, timed with HIP events on the
+launch stream, against the dense MXFP8 MFMA peak. cpu_baseline: the oracle's fp32 attention on the dequantised
+inputs, all host cores, on a bounded sample of the same workload (rank 0, N = 1).
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_MXFP8_TFLOPS = 5000.0      # MI355X dense MXFP8 MFMA peak, published figure (5.0 PFLOP/s)
+PEAK_HBM_GBS = 8000.0           # MI355X HBM3E
+REF_PUBLISHED_TFLOPS = 1811.8   # reference, B4H8S2048 vs128 (docs/perf-matrix.md:41)
+
+WORKLOADS = {
+    # name: (B, H, HK, S, SK, causal, path, splits, description)
+    "cfg2": (4, 8, 8, 2048, 2048, False, "auto", None, "B4H8S2048 non-causal (BASELINE configs[1], vs128)"),
+    "cfg3": (1, 8, 8, 8192, 8192, False, "auto", None, "B1H8S8192 non-causal (configs[2], vs128)"),
+    "cfg4": (2, 8, 8, 2048, 2048, True, "auto", None, "B2H8S2048 causal bottom-right (configs[3])"),
+    "cfg5": (1, 8, 8, 128, 16384, False, "kvsplit", 8, "B1H8 Sq128 SK16384 split 8 (configs[4])"),
+    "cfg1": (1, 1, 1, 256, 256, False, "auto", None, "B1H1S256 (configs[0], t128)"),
+}
+
+
+def flops_of(B, H, S, SK, causal):
+    if not causal:
+        return 4.0 * B * H * S * SK * 128
+    vis = sum(max(0, min(SK, i + SK - S + 1)) for i in range(S))
+    return 4.0 * B * H * vis * 128
+
+
+def cpu_baseline(B, H, HK, S, SK, causal, budget_s=12.0):
+    """fp32 attention on the dequantised inputs (oracle), all host cores, bounded sample: whole (b, h) slices of the
+    workload's shape with the first `rows` query rows, rows chosen so the run takes about `budget_s`."""
+    import oracle
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
+    rows = min(S, 64)
+    secs, _ = oracle.attention_fp32(inp, rows=rows, threads=threads, want_out=False)
+    # scale the sample up to the time budget (never beyond the whole workload)
+    if secs > 0:
+        rows = int(min(S, max(rows, rows * budget_s / max(secs, 1e-3) * 0.5)))
+        secs, _ = oracle.attention_fp32(inp, rows=rows, threads=threads, want_out=False)
+    if causal:
+        vis = sum(max(0, min(SK, i + SK - S + 1)) for i in range(rows))
+        fl = 4.0 * B * H * vis * 128
+    else:
+        fl = 4.0 * B * H * rows * SK * 128
+    return {"value": round(fl / secs / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"fp32 attention on dequantised MXFP8 inputs, B{B} H{H} SK{SK}, first {rows} of {S} query rows of every "
+                      f"(b,h) ({fl / 1e9:.1f} GFLOP in {secs:.2f} s, {threads} threads, oracle/mxfp8_oracle.c)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (the path has no cross-GPU component; --gpus {args.gpus} is not "
+              "supported). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from amdgpu_rustdsl_amd import lib, ops
+
+    B, H, HK, S, SK, causal, path, splits, desc = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    q, k, v, qs, ks, vs = ops.random_inputs(B, H, S, SK, HK=HK, device=dev, seed=1234)
+    out = torch.empty(B, S, H, 128, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    # the first call goes through the torch-facing op (shape checks, workspace); the timed steps call the C-ABI entry
+    # fmha_fwd_hd128_mxfp8_auto directly with the same prepared parameters (dispatch + validate + launch per step)
+    used = ops.fmha_fwd_mxfp8(q, k, v, qs, ks, vs, out, path=path, splits=splits, causal=causal)
+    p = lib.Params()
+    p.o, p.q, p.k, p.v = out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr()
+    p.q_descale, p.k_descale, p.v_descale, p.lse = qs.data_ptr(), ks.data_ptr(), vs.data_ptr(), None
+    p.bytes_q, p.bytes_k, p.bytes_v, p.bytes_o = ops._cap(q), ops._cap(k), ops._cap(v), ops._cap(out)
+    p.bytes_q_descale, p.bytes_k_descale, p.bytes_v_descale = ops._cap(qs), ops._cap(ks), ops._cap(vs)
+    p.B, p.H, p.HK, p.S, p.SK = B, H, HK, S, SK
+    p.path = -1 if path == "auto" else lib.PATH_IDS[path]
+    p.splits, p.causal = splits or 0, int(causal)
+    ws_bytes = lib.workspace_bytes(B, H, S, used[1]) if used[0] == "kvsplit" else 0
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    st = stream.cuda_stream
+
+    def step():
+        return lib.run_auto(p, ws.data_ptr(), ws_bytes, st)
+
+    assert step() == used
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_events = e0.elapsed_time(e1) / args.steps
+    ms_wall = wall * 1e3 / args.steps
+    ms = max(ms_events, ms_wall)
+    fl = flops_of(B, H, S, SK, causal)
+    tflops = fl / (ms * 1e-3) / 1e12
+
+    # dominant kernel alone: launched through the C ABI with a pre-validated kernarg, HIP events on its stream
+    kern_ms = kernel_ms(lib, q, k, v, qs, ks, vs, out, used, B, H, HK, S, SK, causal, stream, args.steps)
+    kern_tflops = fl / (kern_ms * 1e-3) / 1e12
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": "FMHA fwd TFLOP/s + % MXFP8 MFMA peak, hd128 B4H8S2048, 1 MI355X",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(tflops / REF_PUBLISHED_TFLOPS, 4) if args.workload == "cfg2" else None,
+        "dtype": "e4m3 (MXFP8, E8M0/32 scales, fp32 accumulate)",
+        "data": "synthetic: N(0,1) Q/K/V quantised to MXFP8 like the reference's REF_DATA=normal generator, drawn on the GPU",
+        "config": {"workload": f"fmha_fwd_hd128_mxfp8_auto {desc}", "B": B, "H": H, "HK": HK, "S": S, "SK": SK,
+                   "causal": causal, "path": used[0], "splits": used[1], "pct_mxfp8_peak": round(100 * tflops / PEAK_MXFP8_TFLOPS, 2)},
+        "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": PEAK_MXFP8_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(kern_tflops / PEAK_MXFP8_TFLOPS, 4), "traffic": traffic,
+                     "kernel": ("fmha_fwd_hd128_mxfp8_v3_" + used[0]), "kernel_ms": round(kern_ms, 5)},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(B, H, HK, S, SK, causal)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+def kernel_ms(lib, q, k, v, qs, ks, vs, out, used, B, H, HK, S, SK, causal, stream, steps):
+    """Average duration of the main kernel alone (no combine), launched through the C ABI launch entry."""
+    import ctypes
+    import torch
+    from amdgpu_rustdsl_amd.ops import _cap
+    a = lib.fill_args(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), qs.data_ptr(), ks.data_ptr(), vs.data_ptr(),
+                      B, H, HK, S, SK)
+    a.flags = 1 if causal else 0
+    sz = lib.BufferSizes(_cap(q), _cap(k), _cap(v), _cap(out), _cap(qs), _cap(ks), _cap(vs), 0, 0)
+    st = stream.cuda_stream
+    path, nsplit = used
+    if path in ("vs128", "t128"):
+        rows = 256 if path == "vs128" else 128
+        grid = (math.ceil(S / rows), H, B)
+        rc, msg = lib.validate(path, a, sz, grid, HK=HK)
+        assert rc == 0, msg
+        launch = (lambda: lib.raw.fmha_mxfp8_launch_vs128(ctypes.byref(a), *grid, st)) if path == "vs128" else \
+                 (lambda: lib.raw.fmha_mxfp8_launch_t128(ctypes.byref(a), *grid, st))
+    else:
+        rows_total = B * S * H
+        ws = torch.empty(lib.workspace_bytes(B, H, S, nsplit), dtype=torch.uint8, device=q.device)
+        ka = lib.KvsplitArgs()
+        ctypes.memmove(ctypes.addressof(ka), ctypes.addressof(a), 0x270)
+        ka.ptr_ohat = ws.data_ptr()
+        ka.ptr_lse = ws.data_ptr() + nsplit * rows_total * 512
+        ka.kvs_splits, ka.kvs_rows_total = nsplit, rows_total
+        grid = (math.ceil(S / 256), H, B * nsplit)
+        sz.ptr_ohat, sz.ptr_lse = nsplit * rows_total * 512, nsplit * rows_total * 4
+        rc, msg = lib.validate("kvsplit", ka, sz, grid, B=B, HK=HK, KL=0)
+        assert rc == 0, msg
+        launch = lambda: lib.raw.fmha_mxfp8_launch_kvsplit(ctypes.byref(ka), *grid, st)
+    for _ in range(20):
+        assert launch() == 0
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+if __name__ == "__main__":
+    main()
