@@ -123,7 +123,7 @@ uint16_t mxo_pknorm_u16(float x) {
 
 uint8_t mxo_cvt_bf16_fp8(uint16_t bf16, float scale) {
     const float f = mxo_bf16_to_f32(bf16);
-    if (f != f) return 0x7f;
+    if (f != f) return 0xff;   /* gfx950 returns the negative NaN byte for any NaN input */
     const double x = (double)f / (double)scale;
     const uint8_t sgn = (signbit(x) ? 0x80 : 0);
     const double a = fabs(x);
@@ -597,7 +597,8 @@ static void emu_item(const void* vctx, long item) {
     uint16_t* orow = c->out + (((size_t)b * p->S + i) * p->H + h) * D;
     if (c->splits <= 0) {
         emulate_row(p, &rc, b, kvh, qv, sq, 0, p->SK, kvis, &st);
-        const float fin = (1.0f / st.l) * vd;   /* state.rs:79-83 (v_rcp_f32, then x v_descale) */
+        /* state.rs:79-83 (v_rcp_f32, then x v_descale); a row with no visible key (causal extension, S > SK) is 0 */
+        const float fin = st.l > 0.0f ? (1.0f / st.l) * vd : 0.0f;
         for (int d = 0; d < D; ++d) orow[d] = mxo_f32_to_bf16(st.o[d] * fin);
         return;
     }
@@ -612,10 +613,11 @@ static void emu_item(const void* vctx, long item) {
         /* block3.rs:291-356 (Ohat = O * v_descale / l, fp16) and softmax.rs:308-322 (lse = log2(l_total) - 2048 (hi + lo)),
          * with l_total = l / 16 (softmax.rs:277-305): the scaled PV form accumulates O / 16 */
         const float l_total = st.l * 0.0625f;
-        const float fin = (1.0f / l_total) * vd;
+        const float fin = st.l > 0.0f ? (1.0f / l_total) * vd : 0.0f;
         for (int d = 0; d < D; ++d) oh[s][d] = mxo_f32_to_f16((st.o[d] * 0.0625f) * fin);
         const float hl = mxo_f16_to_f32((uint16_t)(st.w & 0xffff)) + mxo_f16_to_f32((uint16_t)(st.w >> 16));
-        lse_s[s] = log2f(l_total) + (hl * 2048.0f) * -1.0f;
+        /* a split without keys gets lse -1e30: weight 0 in the combine */
+        lse_s[s] = st.l > 0.0f ? log2f(l_total) + (hl * 2048.0f) * -1.0f : -1.0e30f;
         if (c->ohat) memcpy(c->ohat + ((size_t)s * rows_total + prow) * D, oh[s], 2 * D);
         if (c->lse) c->lse[(size_t)s * rows_total + prow] = lse_s[s];
     }

@@ -49,7 +49,7 @@ double mxo_e4m3_decode(uint8_t b);
 /* Round-to-nearest-even e4m3 encoder saturating at 448 (ref_host.cpp:216-228). */
 uint8_t mxo_e4m3_encode_sat(float x);
 /* The gfx950 scaled conversion v_cvt_scalef32_pk_fp8_bf16 on one bf16 value:
- * e4m3(RNE(bf16 / scale)), |x| > 464 -> NaN byte (0x7F | sign); NaN -> 0x7F. */
+ * e4m3(RNE(bf16 / scale)), |x| > 464 -> NaN byte (0x7F | sign); NaN -> 0xFF. */
 uint8_t mxo_cvt_bf16_fp8(uint16_t bf16, float scale);
 /* v_cvt_pknorm_u16_f32: round-to-nearest-even of 65535 * clamp(x, 0, 1). */
 uint16_t mxo_pknorm_u16(float x);

@@ -1,0 +1,229 @@
+"""CPU tests of the drop-in boundary (include/fmha_mxfp8.h, libfmha_mxfp8.so): the library loads without a GPU, exports
+every declared entry point, lays the kernargs out at the reference's offsets, and its host contract (validate, path
+selection, workspace size, argument errors of the auto entry) behaves as the reference's
+(tests/gpu/generated/fmha_fwd_hd128_mxfp8_v3_vs128_abi.h:10-209, kvsplit / combine8h headers,
+crates/amdgpu-graph/src/dispatch.rs:494-511). No test here launches a kernel."""
+import ctypes
+import math
+import os
+import re
+
+import pytest
+
+import oracle
+from amdgpu_rustdsl_amd import lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fmha_mxfp8.h")
+
+
+def _declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    src = re.sub(r"//[^\n]*", "", src)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(fmha_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_every_declared_symbol_is_exported():
+    names = _declared_functions()
+    assert "fmha_fwd_hd128_mxfp8_auto" in names and len(names) >= 14
+    for n in names:
+        assert hasattr(lib.raw, n), f"{n} declared in include/fmha_mxfp8.h but not exported"
+    assert sorted(lib.EXPORTED) == names
+
+
+def test_version_string():
+    assert lib.raw.fmha_mxfp8_version().decode().startswith("fmha_mxfp8 gfx950")
+
+
+# vs128_abi.h:10-126 (Args), kvsplit_abi.h (0x270-0x287), combine8h_abi.h (36 B)
+OFFSETS = {
+    "ptr_o": 0x000, "ptr_q": 0x010, "ptr_k": 0x020, "ptr_v": 0x030, "ptr_lse": 0x040, "softmax_scale": 0x050,
+    "s_seq_len": 0x060, "s_Seqs": 0x070, "s_Hs": 0x090, "s_Bs": 0x0A0, "s_gqa": 0x0B0, "s_k_Seqs": 0x0C0,
+    "s_k_Hs": 0x0D0, "s_k_Bs": 0x0E0, "opt": 0x0F0, "s_kv_seq_len": 0x110, "s_q_head_num": 0x140, "s_v_Seqs": 0x150,
+    "s_v_Hs": 0x160, "s_v_Bs": 0x170, "s_o_Seqs": 0x180, "s_o_Hs": 0x190, "s_o_Bs": 0x1A0, "ptr_q_descale": 0x200,
+    "ptr_k_descale": 0x210, "ptr_v_descale": 0x220, "s_descale_q_Bs": 0x230, "s_descale_q_Hs": 0x240,
+    "s_descale_k_Bs": 0x250, "s_descale_k_Hs": 0x260, "flags": 0x280,
+}
+
+
+def test_kernarg_layouts():
+    assert ctypes.sizeof(lib.Args) == 656 and ctypes.sizeof(lib.KvsplitArgs) == 648 and ctypes.sizeof(lib.CombineArgs) == 36
+    for name, off in OFFSETS.items():
+        assert getattr(lib.Args, name).offset == off, name
+    assert lib.KvsplitArgs.ptr_ohat.offset == 0x270 and lib.KvsplitArgs.ptr_lse.offset == 0x278
+    assert lib.KvsplitArgs.kvs_splits.offset == 0x280 and lib.KvsplitArgs.kvs_rows_total.offset == 0x284
+    assert [lib.CombineArgs.ptr_ohat.offset, lib.CombineArgs.ptr_lse.offset, lib.CombineArgs.ptr_out.offset,
+            lib.CombineArgs.rows_total.offset, lib.CombineArgs.d.offset, lib.CombineArgs.splits.offset] == [0, 8, 16, 24, 28, 32]
+
+
+def _shape_args(B=2, H=8, HK=4, S=300, SK=700):
+    a = lib.fill_args(0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 0x6000, 0x7000, B, H, HK, S, SK)
+    sz = lib.BufferSizes(B * S * H * 128, B * SK * HK * 128, B * SK * HK * 128, B * S * H * 256,
+                         B * S * H * 4 + 2048 * H, B * SK * HK * 4 + 2560 * H, 4096, 0, 0)
+    return a, sz
+
+
+def test_fill_args_values():
+    """ref_host.cpp:272-330 packing: strides in bytes, head strides 128 / 256 / 4, gqa = H / HK, opt = 5."""
+    B, H, HK, S, SK = 2, 8, 4, 300, 700
+    a, _ = _shape_args(B, H, HK, S, SK)
+    assert (a.ptr_o, a.ptr_q, a.ptr_k, a.ptr_v, a.ptr_q_descale, a.ptr_k_descale, a.ptr_v_descale) == \
+        (0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 0x6000, 0x7000)
+    assert (a.s_seq_len, a.s_kv_seq_len, a.s_q_head_num, a.s_gqa) == (S, SK, H, H // HK)
+    assert (a.s_Seqs, a.s_Hs, a.s_Bs) == (H * 128, 128, S * H * 128)
+    assert (a.s_k_Seqs, a.s_k_Hs, a.s_k_Bs) == (HK * 128, 128, SK * HK * 128)
+    assert (a.s_v_Seqs, a.s_v_Hs, a.s_v_Bs) == (HK * 128, 128, SK * HK * 128)
+    assert (a.s_o_Seqs, a.s_o_Hs, a.s_o_Bs) == (H * 256, 256, S * H * 256)
+    assert (a.s_descale_q_Bs, a.s_descale_q_Hs, a.s_descale_k_Bs, a.s_descale_k_Hs) == (S * H * 4, 4, SK * HK * 4, 4)
+    assert a.flags == 0 and a.ptr_lse is None
+
+
+@pytest.mark.parametrize("kind,rows", [("vs128", 256), ("t128", 128)])
+def test_validate_accepts_consistent_launch(kind, rows):
+    a, sz = _shape_args()
+    assert lib.validate(kind, a, sz, (math.ceil(300 / rows), 8, 2), HK=4) == (0, "")
+
+
+# (mutation, expected code, message fragment) in the reference's rule order
+NEGATIVE = [
+    (lambda a, sz, g: setattr(sz, "ptr_q", sz.ptr_q - 1), lib.FMHA_ERR_EXTENT, "ptr_q"),
+    (lambda a, sz, g: setattr(sz, "ptr_o", 10), lib.FMHA_ERR_EXTENT, "ptr_o"),
+    (lambda a, sz, g: setattr(sz, "ptr_q_descale", sz.ptr_q_descale - 1), lib.FMHA_ERR_EXTENT, "ptr_q_descale"),
+    (lambda a, sz, g: setattr(sz, "ptr_k_descale", sz.ptr_k_descale - 1), lib.FMHA_ERR_EXTENT, "ptr_k_descale"),
+    (lambda a, sz, g: setattr(sz, "ptr_v_descale", 4095), lib.FMHA_ERR_EXTENT, "ptr_v_descale"),
+    (lambda a, sz, g: setattr(a, "s_gqa", 0), lib.FMHA_ERR_KA_RANGE, "0xB0"),
+    (lambda a, sz, g: setattr(a, "s_gqa", 32), lib.FMHA_ERR_KA_RANGE, "0xB0"),
+    (lambda a, sz, g: setattr(a, "s_Hs", 64), lib.FMHA_ERR_KA_RANGE, "0x90"),
+    (lambda a, sz, g: setattr(a, "s_o_Hs", 128), lib.FMHA_ERR_KA_RANGE, "0x190"),
+    (lambda a, sz, g: setattr(a, "s_descale_k_Hs", 8), lib.FMHA_ERR_KA_RANGE, "0x260"),
+    (lambda a, sz, g: setattr(a, "s_gqa", 4), lib.FMHA_ERR_KA_IS, "0x140"),
+    (lambda a, sz, g: setattr(a, "s_Seqs", 1000), lib.FMHA_ERR_KA_IS, "0x70"),
+    (lambda a, sz, g: setattr(a, "s_v_Seqs", 128), lib.FMHA_ERR_KA_IS, "0x150"),
+    (lambda a, sz, g: setattr(a, "s_descale_k_Bs", 4), lib.FMHA_ERR_KA_IS, "0x250"),
+    (lambda a, sz, g: g.__setitem__(1, 7), lib.FMHA_ERR_GRID, "axis 1"),
+    (lambda a, sz, g: g.__setitem__(0, 1), lib.FMHA_ERR_GRID, "axis 0"),
+]
+
+
+@pytest.mark.parametrize("i", range(len(NEGATIVE)))
+def test_validate_rejects(i):
+    mutate, code, frag = NEGATIVE[i]
+    a, sz = _shape_args()
+    g = [math.ceil(300 / 256), 8, 2]
+    mutate(a, sz, g)
+    rc, msg = lib.validate("vs128", a, sz, tuple(g), HK=4)
+    assert rc == code and frag in msg, (rc, msg)
+    assert msg.startswith("GV-HOST-")
+
+
+def _kvsplit(B=1, H=8, HK=8, S=128, SK=16384, splits=8):
+    a, sz = _shape_args(B, H, HK, S, SK)
+    ka = lib.KvsplitArgs()
+    ctypes.memmove(ctypes.addressof(ka), ctypes.addressof(a), 0x270)
+    rows = B * S * H
+    ka.ptr_ohat, ka.ptr_lse, ka.kvs_splits, ka.kvs_rows_total = 0x8000, 0x9000, splits, rows
+    sz.ptr_ohat, sz.ptr_lse = splits * rows * 512, splits * rows * 4
+    return ka, sz, (math.ceil(S / 256), H, B * splits)
+
+
+def test_validate_kvsplit():
+    ka, sz, g = _kvsplit()
+    assert lib.validate("kvsplit", ka, sz, g, B=1, HK=8, KL=0) == (0, "")
+    ka2, sz2, _ = _kvsplit()
+    sz2.ptr_ohat -= 1
+    assert lib.validate("kvsplit", ka2, sz2, g, B=1, HK=8)[0] == lib.FMHA_ERR_EXTENT
+    ka3, sz3, _ = _kvsplit()
+    ka3.kvs_rows_total += 1
+    rc, msg = lib.validate("kvsplit", ka3, sz3, g, B=1, HK=8)
+    assert rc == lib.FMHA_ERR_EXTENT or (rc == lib.FMHA_ERR_KA_IS and "0x284" in msg)
+    ka4, sz4, _ = _kvsplit()
+    ka4.kvs_rows_total += 1
+    sz4.ptr_ohat, sz4.ptr_lse = 1 << 40, 1 << 40
+    rc, msg = lib.validate("kvsplit", ka4, sz4, g, B=1, HK=8)
+    assert rc == lib.FMHA_ERR_KA_IS and "0x284" in msg
+    ka5, sz5, _ = _kvsplit()
+    assert lib.validate("kvsplit", ka5, sz5, (g[0], g[1], 4), B=1, HK=8)[0] == lib.FMHA_ERR_GRID
+    ka6, sz6, _ = _kvsplit()
+    ka6.kvs_splits = 0
+    assert lib.validate("kvsplit", ka6, sz6, g, B=1, HK=8)[0] == lib.FMHA_ERR_KA_RANGE
+    assert lib.validate("kvsplit", ka, sz, g, B=1, HK=8, KL=-1)[0] == lib.FMHA_ERR_SYM
+
+
+def test_validate_combine():
+    ca = lib.CombineArgs(0x1, 0x2, 0x3, 1024, 128, 8)
+    sz = lib.BufferSizes(0, 0, 0, 1024 * 256, 0, 0, 0, 8 * 1024 * 512, 8 * 1024 * 4)
+    assert lib.validate("combine", ca, sz, (64, 1, 1)) == (0, "")
+    ca.d = 64
+    assert lib.validate("combine", ca, sz, (64, 1, 1))[0] == lib.FMHA_ERR_KA_RANGE
+    ca.d = 128
+    sz.ptr_o -= 1
+    assert lib.validate("combine", ca, sz, (64, 1, 1))[0] == lib.FMHA_ERR_EXTENT
+
+
+def test_select_path_matches_oracle():
+    """The host dispatch (C++) and the oracle's restatement (C) agree on a grid of shapes, including the empty-split
+    exclusion (dispatch.rs:494-511)."""
+    for B in (1, 2, 3, 4, 8):
+        for H in (1, 2, 8, 16, 64):
+            for S in (1, 77, 128, 256, 257, 1000, 2048, 8192):
+                for SK in (1, 100, 1337, 2048, 2049, 4096, 16000, 16384, 20000):
+                    assert lib.select_path(B, H, S, SK) == oracle.select_path(B, H, S, SK), (B, H, S, SK)
+    # published choices (docs/perf-matrix.md:31-55)
+    assert lib.select_path(1, 8, 2048, 2048) == ("kvsplit", 4)
+    assert lib.select_path(1, 8, 4096, 4096) == ("kvsplit", 2)
+    assert lib.select_path(4, 8, 2048, 2048)[0] == "vs128"
+    assert lib.select_path(4, 8, 512, 512)[0] == "t128"
+    assert lib.select_path(1, 8, 128, 16384) == ("kvsplit", 4)
+
+
+def test_workspace_bytes():
+    for B, H, S, sp in ((1, 8, 128, 8), (4, 8, 2048, 2), (3, 5, 77, 4)):
+        assert lib.workspace_bytes(B, H, S, sp) == sp * B * S * H * (512 + 4)
+
+
+def _params(**kw):
+    p = lib.Params()
+    p.B, p.H, p.HK, p.S, p.SK = kw.get("B", 1), kw.get("H", 8), kw.get("HK", 8), kw.get("S", 128), kw.get("SK", 4096)
+    p.path, p.splits, p.causal = kw.get("path", -1), kw.get("splits", 0), kw.get("causal", 0)
+    big = 1 << 40
+    p.o = p.q = p.k = p.v = p.q_descale = p.k_descale = p.v_descale = 0x1000
+    p.bytes_q = p.bytes_k = p.bytes_v = p.bytes_o = p.bytes_q_descale = p.bytes_k_descale = p.bytes_v_descale = big
+    return p
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(H=6, HK=4), lib.FMHA_ERR_KA_RANGE),              # H not a power-of-two multiple of HK
+    (dict(H=64, HK=2), lib.FMHA_ERR_KA_RANGE),             # gqa 32 > 16
+    (dict(S=0), lib.FMHA_ERR_KA_RANGE),
+    (dict(path=7), lib.FMHA_ERR_PATH),
+    (dict(path=2, splits=3), lib.FMHA_ERR_PATH),            # splits not in {2, 4, 8}
+    (dict(path=2, splits=8, SK=4224), lib.FMHA_ERR_PATH),   # 33 tiles, 5 per split: split 7 would start past the end
+    (dict(path=2, splits=4, causal=1), lib.FMHA_ERR_PATH),  # no causal on the KV split
+])
+def test_auto_rejects_before_any_gpu_work(kw, code):
+    """fmha_fwd_hd128_mxfp8_auto checks its arguments before touching the device (these run without a GPU)."""
+    p = _params(**kw)
+    err = ctypes.create_string_buffer(256)
+    po, so = ctypes.c_int(-1), ctypes.c_int(-1)
+    rc = lib.raw.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(p), None, 0, None, ctypes.byref(po), ctypes.byref(so), err, 256)
+    assert rc == code, (rc, err.value)
+
+
+def test_auto_requires_workspace():
+    """The KV-split path needs the caller's workspace of fmha_mxfp8_workspace_bytes (no allocation in the library)."""
+    p = _params(path=2, splits=4, SK=4096)
+    err = ctypes.create_string_buffer(256)
+    po, so = ctypes.c_int(-1), ctypes.c_int(-1)
+    rc = lib.raw.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(p), None, 10, None, ctypes.byref(po), ctypes.byref(so), err, 256)
+    assert rc == lib.FMHA_ERR_WORKSPACE, (rc, err.value)
+
+
+def test_init_without_gpu_reports_error():
+    """With no device the library reports FMHA_ERR_NO_DEVICE / FMHA_ERR_HIP instead of crashing."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    err = ctypes.create_string_buffer(256)
+    rc = lib.raw.fmha_mxfp8_init(err, 256)
+    assert rc in (lib.FMHA_ERR_NO_DEVICE, lib.FMHA_ERR_HIP) and err.value
