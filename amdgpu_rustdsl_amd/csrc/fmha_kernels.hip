@@ -23,6 +23,7 @@
 // ds_read_b128 K reads and the transposing V reads bank-conflict free.
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #include "../../include/fmha_mxfp8.h"
@@ -64,17 +65,53 @@ struct Prm {
     uint8_t* ohat;
     float* lse;
     uint32_t splits, rows_total;
+#ifdef FMHA_TRACE
+    uint64_t* trace;   // debug builds only: per (block, wave) timestamps, pointer at kernarg 0x288
+    uint64_t t_entry;  // timestamp of the kernel's first instruction
+#endif
 };
 
-__device__ inline Prm prm_from(const fmha_mxfp8_args& a) {
+// Debug builds (-DFMHA_TRACE) record s_memrealtime (100 MHz) at phase boundaries: slot i of wave w of logical block
+// blk at trace[(blk * 8 + w) * 8 + i], written by lane 0 with a vector store. Release builds compile it away.
+#ifdef FMHA_TRACE
+#define FMHA_MARK(p, blk, i)                                                                                  \
+    do {                                                                                                    \
+        if ((p).trace && (threadIdx.x & 63u) == 0u)                                                         \
+            (p).trace[((size_t)(blk) * 8u + (threadIdx.x >> 6)) * 8u + (i)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define FMHA_MARK(p, blk, i) do { } while (0)
+#endif
+
+#define KA_AS __attribute__((address_space(4)))
+
+// The kernel arguments are read field by field through the kernarg segment pointer, in the constant address space and
+// at each field's natural alignment: scalar loads through the scalar cache. (Through the by-value parameter of the
+// packed ABI struct the compiler cannot prove alignment and emits vector loads per field and wave, which for 2048 waves
+// took microseconds before the first tile.)
+template <typename T>
+__device__ inline T ka(uint32_t off) {
+    return *(const KA_AS T*)((const KA_AS uint8_t*)__builtin_amdgcn_kernarg_segment_ptr() + off);
+}
+#define KA_FIELD(T, field) ka<T>(offsetof(fmha_mxfp8_args, field))
+
+__device__ inline Prm prm_from_kernarg() {
     Prm p;
-    p.q = (const uint8_t*)a.ptr_q; p.k = (const uint8_t*)a.ptr_k; p.v = (const uint8_t*)a.ptr_v;
-    p.qs = (const uint8_t*)a.ptr_q_descale; p.ks = (const uint8_t*)a.ptr_k_descale; p.vd = (const float*)a.ptr_v_descale;
-    p.o = (uint8_t*)a.ptr_o; p.lse_out = (float*)a.ptr_lse;
-    p.S = a.s_seq_len; p.SK = a.s_kv_seq_len; p.H = a.s_q_head_num; p.gqa = a.s_gqa; p.flags = a.flags;
-    p.q_seq = a.s_Seqs; p.q_b = a.s_Bs; p.k_seq = a.s_k_Seqs; p.k_b = a.s_k_Bs; p.v_seq = a.s_v_Seqs; p.v_b = a.s_v_Bs;
-    p.o_seq = a.s_o_Seqs; p.o_b = a.s_o_Bs; p.qs_b = a.s_descale_q_Bs; p.ks_b = a.s_descale_k_Bs;
+    p.q = (const uint8_t*)KA_FIELD(uint64_t, ptr_q); p.k = (const uint8_t*)KA_FIELD(uint64_t, ptr_k);
+    p.v = (const uint8_t*)KA_FIELD(uint64_t, ptr_v);
+    p.qs = (const uint8_t*)KA_FIELD(uint64_t, ptr_q_descale); p.ks = (const uint8_t*)KA_FIELD(uint64_t, ptr_k_descale);
+    p.vd = (const float*)KA_FIELD(uint64_t, ptr_v_descale);
+    p.o = (uint8_t*)KA_FIELD(uint64_t, ptr_o); p.lse_out = (float*)KA_FIELD(uint64_t, ptr_lse);
+    p.S = KA_FIELD(uint32_t, s_seq_len); p.SK = KA_FIELD(uint32_t, s_kv_seq_len); p.H = KA_FIELD(uint32_t, s_q_head_num);
+    p.gqa = KA_FIELD(uint32_t, s_gqa); p.flags = KA_FIELD(uint32_t, flags);
+    p.q_seq = KA_FIELD(uint32_t, s_Seqs); p.q_b = KA_FIELD(uint32_t, s_Bs); p.k_seq = KA_FIELD(uint32_t, s_k_Seqs);
+    p.k_b = KA_FIELD(uint32_t, s_k_Bs); p.v_seq = KA_FIELD(uint32_t, s_v_Seqs); p.v_b = KA_FIELD(uint32_t, s_v_Bs);
+    p.o_seq = KA_FIELD(uint32_t, s_o_Seqs); p.o_b = KA_FIELD(uint32_t, s_o_Bs);
+    p.qs_b = KA_FIELD(uint32_t, s_descale_q_Bs); p.ks_b = KA_FIELD(uint32_t, s_descale_k_Bs);
     p.ohat = nullptr; p.lse = nullptr; p.splits = 1; p.rows_total = 0;
+#ifdef FMHA_TRACE
+    p.trace = (uint64_t*)(uintptr_t)(ka<uint32_t>(0x288) | ((uint64_t)ka<uint32_t>(0x28C) << 32));
+#endif
     return p;
 }
 
@@ -123,62 +160,60 @@ __device__ inline void lds_write4(uint32_t off, uint32_t v) { *(LDS_AS uint32_t*
 // slot: load() issues the buffer loads into VGPRs, store() writes them (after the slot is free) with ds_write_b128.
 // Thread tid moves 16-byte chunk (tid & 7) of rows i NT/8 + tid/8, i < kN: each 8-thread group reads one
 // contiguous 128-byte row. The chunk lands at (chunk ^ swz(row)); NT/8 is a multiple of 16, so the swizzle and
-// the per-thread offsets are the same for every i and the tile's first key rides in the scalar offset.
-// (Staging through VGPRs instead of buffer_load ... lds keeps every LDS read free of the compiler's
-// conservative vmcnt(0) before reads that might alias an in-flight LDS DMA.)
+// the per-thread offsets are the same for every i.
+// The tile's first key rides in the buffer resource's base and the resource's size ends at the sequence's last key,
+// so rows past the end (the last, partial tile) read zeros from the range check, and a tile index past the range
+// gets an empty resource (no memory traffic): one branch-free code path, so the compiler keeps a single register set
+// for the staged tile (merging several sets cost a copy behind a wait for every load, which serialised the prefetch).
+// (Staging through VGPRs instead of buffer_load ... lds keeps every LDS read free of the compiler's conservative
+// vmcnt(0) before reads that might alias an in-flight LDS DMA.)
 template <int NT>
 struct Stager {
     static constexpr int kN = kTileBytes / (NT * 16);   // 16-byte chunks per thread per 16 KiB tile
-    __amdgpu_buffer_rsrc_t rk, rv, rks;
-    uint32_t voff;     // (tid / 8) k_seq + 16 (tid & 7)
-    uint32_t woff;     // (tid / 8) 128 + 16 ((tid & 7) ^ swz(tid / 8))
+    const uint8_t *kb, *vb, *ksb;
+    uint32_t voff[kN];  // (i NT/8 + tid/8) k_seq + 16 (tid & 7)
+    uint32_t ksoff;     // tid ks_row
+    uint32_t woff;      // (tid / 8) 128 + 16 ((tid & 7) ^ swz(tid / 8))
     uint32_t tid, k_seq, ks_row, SK, lds;
     v4i kr[kN], vr[kN];
     uint32_t ksr;
 
-    __device__ void init(const uint8_t* kb, const uint8_t* vb, const uint8_t* ksb, uint32_t kv_bytes, uint32_t ks_bytes,
-                         uint32_t k_seq_, uint32_t SK_, uint32_t lds_) {
-        rk = make_rsrc(kb, kv_bytes);
-        rv = make_rsrc(vb, kv_bytes);
-        rks = make_rsrc(ksb, ks_bytes);
+    __device__ void init(const uint8_t* kb_, const uint8_t* vb_, const uint8_t* ksb_, uint32_t k_seq_, uint32_t SK_, uint32_t lds_) {
+        kb = kb_; vb = vb_; ksb = ksb_;
         tid = threadIdx.x;
         k_seq = k_seq_;
         ks_row = k_seq_ >> 5;
         SK = SK_;
         lds = lds_;
         const uint32_t row = tid >> 3, c = tid & 7u;
-        voff = row * k_seq + (c << 4);
+#pragma unroll
+        for (int i = 0; i < kN; ++i) voff[i] = (row + (uint32_t)(i * NT / 8)) * k_seq + (c << 4);
+        ksoff = tid * ks_row;
         woff = row * 128u + ((c ^ swz(row)) << 4);
     }
 
-    __device__ __forceinline__ void load(uint32_t key0) {
-        if (key0 + (uint32_t)kTile <= SK) {
+    // Loads tile [key0, key0 + 128) when `valid` (zeros past SK), nothing when not.
+    __device__ __forceinline__ void load(uint32_t key0, bool valid) {
+        const uint32_t left = valid ? SK - key0 : 0u;   // keys left in the sequence from key0 (>= 1 when valid)
+        const uint32_t kvb = left ? (left - 1u) * k_seq + kD : 0u;
+        const uint32_t ksb_bytes = left ? (left - 1u) * ks_row + 4u : 0u;
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb + (size_t)key0 * k_seq, kvb);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + (size_t)key0 * k_seq, kvb);
+        const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksb + (size_t)key0 * ks_row, ksb_bytes);
 #pragma unroll
-            for (int i = 0; i < kN; ++i) {
-                const uint32_t so = (key0 + (uint32_t)(i * NT / 8)) * k_seq;
-                kr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rk, voff, so, 0));
-                vr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, so, 0));
-            }
-            if (tid < 128u) ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, tid * ks_row, key0 * ks_row, 0);
-        } else {
-            // the last, partial tile: rows past the sequence end re-read the last key (masked in the softmax)
-#pragma unroll
-            for (int i = 0; i < kN; ++i) {
-                const uint32_t key = min(key0 + (uint32_t)(i * NT / 8) + (tid >> 3), SK - 1u);
-                const uint32_t off = key * k_seq + ((tid & 7u) << 4);
-                kr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-                vr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
-            }
-            if (tid < 128u) ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, min(key0 + tid, SK - 1u) * ks_row, 0, 0);
+        for (int i = 0; i < kN; ++i) {
+            kr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rk, voff[i], 0, 0));
+            vr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, voff[i], 0, 0));
         }
+        ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, tid < 128u ? ksoff : 0x80000000u, 0, 0);
     }
 
     __device__ __forceinline__ void store(uint32_t slot) const {
-        const uint32_t kb = slot_base(lds, kLdsK, slot, kTileBytes) + woff, vb = slot_base(lds, kLdsV, slot, kTileBytes) + woff;
+        const uint32_t kb_ = slot_base(lds, kLdsK, slot, kTileBytes) + woff, vb_ = slot_base(lds, kLdsV, slot, kTileBytes) + woff;
 #pragma unroll
         for (int i = 0; i < kN; ++i) {
-            lds_write16(kb + i * NT * 16, kr[i]);
-            lds_write16(vb + i * NT * 16, vr[i]);
+            lds_write16(kb_ + i * NT * 16, kr[i]);
+            lds_write16(vb_ + i * NT * 16, vr[i]);
         }
         if (tid < 128u) lds_write4(slot_base(lds, kLdsKs, slot, 512u) + tid * 4u, ksr);
     }
@@ -501,8 +536,15 @@ __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint
     constexpr int NT = 512;
     const Recipe rc = LUT ? Recipe{120.0f / 512.0f, 131.0f / 512.0f, 1.0f}
                           : Recipe{__builtin_bit_cast(float, 0x3e85d086u), __builtin_bit_cast(float, 0x3e7df17eu), 0.25f};
+    const uint32_t tblk = ((bidx * p.splits + split) * p.H + head) * ((p.S + 255u) / 256u) + qtile;
+    (void)tblk;
+    FMHA_MARK(p, tblk, 0);
+#ifdef FMHA_TRACE
+    if (p.trace && (threadIdx.x & 63u) == 0u) p.trace[((size_t)tblk * 8u + (threadIdx.x >> 6)) * 8u + 7u] = p.t_entry;
+#endif
     Wave<NT> w;
     w.init(p, lds, qtile, head, bidx, key_hi);
+    FMHA_MARK(p, tblk, 1);
     const bool grp_b = w.wave >= 4u;
     const uint32_t kvh = head / p.gqa;
     const bool causal = (p.flags & 1u) != 0;
@@ -512,27 +554,31 @@ __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint
 
     Stager<NT> st;
     st.init(p.k + (size_t)bidx * p.k_b + kvh * kD, p.v + (size_t)bidx * p.v_b + kvh * kD, p.ks + (size_t)bidx * p.ks_b + kvh * 4u,
-            (p.SK - 1u) * p.k_seq + kD, (p.SK - 1u) * (p.k_seq >> 5) + 4u, p.k_seq, p.SK, lds);
+            p.k_seq, p.SK, lds);
     auto slot_of = [](uint32_t t) { return t % 3u; };
     auto key_of = [&](uint32_t t) { return key_lo + t * kTile; };
 
     v16f s[4];
     if (ntiles > 0) {
-        st.load(key_of(0));
+        st.load(key_of(0), true);
         st.store(0);
-        if (ntiles > 1) {
-            st.load(key_of(1));
-            if (grp_b) st.store(1);      // A keeps its share of tile 1 for V(0)
-        }
-        if (grp_b && ntiles > 2) st.load(key_of(2));
+        st.load(key_of(1), ntiles > 1);
+        if (grp_b && ntiles > 1) st.store(1);
+        // in registers at the loop's entry: A its share of tile 1 (stored in V(0)), B of tile 2 (one load for both,
+        // so the staged registers have a single definition)
+        const uint32_t tp = grp_b ? 2u : 1u;
+        st.load(key_of(tp), tp < ntiles);
+        FMHA_MARK(p, tblk, 2);
         block_barrier();
+        FMHA_MARK(p, tblk, 3);
         if (w.active(key_of(0))) w.qk_all(0, s);
         if (grp_b) block_barrier();      // B starts one phase behind
         for (uint32_t t = 0; t < ntiles; ++t) {
             // ---- V(t)
             __builtin_amdgcn_s_setprio(0);
-            if (!grp_b && t + 1 < ntiles) st.store(slot_of(t + 1));
-            if (grp_b && t + 2 < ntiles) st.store(slot_of(t + 2));
+            // A stores its share of tile t+1, B of tile t+2 (one uniform index: a single code path)
+            const uint32_t ts = t + (grp_b ? 2u : 1u);
+            if (ts < ntiles) st.store(slot_of(ts));
             const bool act = w.active(key_of(t));
             uint32_t pw[4][4];
             if (act) {
@@ -545,15 +591,17 @@ __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint
             // ---- M(t): PV(t), then (P dead) the staging loads, then QK(t+1)
             __builtin_amdgcn_s_setprio(1);
             if (act) w.pv_all(slot_of(t), pw);
-            if (!grp_b && t + 2 < ntiles) st.load(key_of(t + 2));
-            if (grp_b && t + 3 < ntiles) st.load(key_of(t + 3));
+            const uint32_t tl = t + (grp_b ? 3u : 2u);
+            st.load(key_of(tl), tl < ntiles);
             if (t + 1 < ntiles && w.active(key_of(t + 1))) w.qk_all(slot_of(t + 1), s);
             block_barrier();
         }
         if (!grp_b) block_barrier();     // A ends one phase ahead: the barrier counts match
         __builtin_amdgcn_s_setprio(0);
     }
+    FMHA_MARK(p, tblk, 4);
     epilogue<SPLIT>(p, w, head, bidx, split, rc);
+    FMHA_MARK(p, tblk, 5);
 }
 
 // One 4-wave group (_t128: one wave per SIMD, so each wave overlaps its own VALU with its own MFMAs): S(t) is
@@ -575,17 +623,15 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
     const uint32_t ntiles = key_end > key_lo ? (key_end - key_lo + kTile - 1) / kTile : 0;
     Stager<NT> st;
     st.init(p.k + (size_t)bidx * p.k_b + kvh * kD, p.v + (size_t)bidx * p.v_b + kvh * kD, p.ks + (size_t)bidx * p.ks_b + kvh * 4u,
-            (p.SK - 1u) * p.k_seq + kD, (p.SK - 1u) * (p.k_seq >> 5) + 4u, p.k_seq, p.SK, lds);
+            p.k_seq, p.SK, lds);
     auto key_of = [&](uint32_t t) { return key_lo + t * kTile; };
 
     v16f s[4];
     if (ntiles > 0) {
-        st.load(key_of(0));
+        st.load(key_of(0), true);
         st.store(0);
-        if (ntiles > 1) {
-            st.load(key_of(1));
-            st.store(1);
-        }
+        st.load(key_of(1), ntiles > 1);
+        if (ntiles > 1) st.store(1);
         block_barrier();
         if (w.active(key_of(0))) {
             w.qk_all(0, s);
@@ -596,7 +642,7 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
         for (uint32_t t = 0; t + 1 < ntiles; ++t) {
             const uint32_t nslot = slot == 2u ? 0u : slot + 1u;
             const uint32_t sslot = nslot == 2u ? 0u : nslot + 1u;   // slot of tile t+2
-            if (t + 2 < ntiles) st.load(key_of(t + 2));
+            st.load(key_of(t + 2), t + 2 < ntiles);
             const bool act = w.active(key_of(t)), act_next = w.active(key_of(t + 1));
             uint32_t pw[4][4];
             if (act_next) {
@@ -640,30 +686,33 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
     epilogue<false>(p, w, head, bidx, 0, rc);
 }
 
-// Workgroup -> (q tile, head, z): consecutive tiles of one (batch, head) land on one XCD (the hardware deals
-// workgroups round-robin over the 8 XCDs), so each XCD's L2 holds the K/V its blocks share.
-__device__ inline void block_coords(uint32_t& qt, uint32_t& head, uint32_t& z) {
-    // grid extents from the AQL dispatch packet (grid_size in work-items at byte 12/16/20, workgroup_size at 4/6/8),
-    // so the kernels need no hidden kernel arguments: the kernarg segment is exactly the reference's
-    const uint8_t __attribute__((address_space(4)))* pk = (const uint8_t __attribute__((address_space(4)))*)__builtin_amdgcn_dispatch_ptr();
-    const uint32_t wgx = *(const uint16_t __attribute__((address_space(4)))*)(pk + 4);
-    const uint32_t gx = *(const uint32_t __attribute__((address_space(4)))*)(pk + 12) / wgx;
-    const uint32_t gy = *(const uint32_t __attribute__((address_space(4)))*)(pk + 16);
-    const uint32_t gz = *(const uint32_t __attribute__((address_space(4)))*)(pk + 20);
-    const uint32_t nblk = gx * gy * gz;
-    uint32_t L = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
-    if ((nblk & 7u) == 0u) L = (L & 7u) * (nblk >> 3) + (L >> 3);
+// Workgroup -> (q tile, head, z): consecutive tiles of one (batch, head) land on one XCD, so each XCD's L2 holds the K/V
+// its blocks share. The hardware deals workgroups round-robin over the 8 XCDs in linear order x + gx (y + gy z); when
+// n = gx gy is a multiple of 8 that XCD is (x + gx y) mod 8 in every z slice, and L -> (L mod 8) (n / 8) + L / 8
+// gives XCD k the slice's logical blocks [k n / 8, (k + 1) n / 8). The grid extents come from the kernel arguments
+// (gx = ceil(S / rows), gy = H): reading them from the dispatch packet, which sits in the host-memory queue, cost every
+// wave a round trip over PCIe at start-up (microseconds, growing with the wave count).
+__device__ inline void block_coords(uint32_t S, uint32_t H, uint32_t rows, uint32_t& qt, uint32_t& head, uint32_t& z) {
+    const uint32_t gx = (S + rows - 1u) / rows;
+    const uint32_t n = gx * H;
+    uint32_t L = blockIdx.x + gx * blockIdx.y;
+    if ((n & 7u) == 0u) L = (L & 7u) * (n >> 3) + (L >> 3);
     qt = __builtin_amdgcn_readfirstlane(L % gx);
-    const uint32_t rest = L / gx;
-    head = __builtin_amdgcn_readfirstlane(rest % gy);
-    z = __builtin_amdgcn_readfirstlane(rest / gy);
+    head = __builtin_amdgcn_readfirstlane(L / gx);
+    z = blockIdx.z;
 }
 
 template <int NT>
-__device__ void full_kernel(const fmha_mxfp8_args& a, uint32_t lds) {
-    const Prm p = prm_from(a);
+__device__ void full_kernel(uint32_t lds) {
+#ifdef FMHA_TRACE
+    const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();
+    Prm p = prm_from_kernarg();
+    p.t_entry = t_entry;
+#else
+    const Prm p = prm_from_kernarg();
+#endif
     uint32_t qt, head, z;
-    block_coords(qt, head, z);
+    block_coords(p.S, p.H, NT / 2, qt, head, z);
     const bool lut = (p.SK + 127u) / 128u < 4u;   // state.rs:75-77
     if (NT == 512) {
         if (lut) attend_pingpong<true, false>(p, lds, qt, head, z, 0, 0, p.SK);
@@ -682,26 +731,28 @@ __device__ void full_kernel(const fmha_mxfp8_args& a, uint32_t lds) {
 
 extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_vs128(fmha_mxfp8_args a) {
     FMHA_LDS_BASE(smem);
-    full_kernel<512>(a, smem_base);
+    (void)a;   // read through kernarg()
+    full_kernel<512>(smem_base);
 }
 
 extern "C" __global__ void __launch_bounds__(256, 1) fmha_fwd_hd128_mxfp8_v3_t128(fmha_mxfp8_args a) {
     FMHA_LDS_BASE(smem);
-    full_kernel<256>(a, smem_base);
+    (void)a;
+    full_kernel<256>(smem_base);
 }
 
-extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvsplit(fmha_mxfp8_kvsplit_args ka) {
+extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvsplit(fmha_mxfp8_kvsplit_args ka_) {
     FMHA_LDS_BASE(smem);
-    const fmha_mxfp8_args& a = *reinterpret_cast<const fmha_mxfp8_args*>(&ka);   // bytes 0x000..0x26F are the base layout
-    Prm p = prm_from(a);
+    (void)ka_;   // read through ka<>(); bytes 0x000..0x26F are the base layout
+    Prm p = prm_from_kernarg();
     p.flags = 0;   // 0x280 holds the split count in this layout
     p.lse_out = nullptr;
-    p.ohat = (uint8_t*)ka.ptr_ohat;
-    p.lse = (float*)ka.ptr_lse;
-    p.splits = ka.kvs_splits;
-    p.rows_total = ka.kvs_rows_total;
+    p.ohat = (uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_kvsplit_args, ptr_ohat));
+    p.lse = (float*)ka<uint64_t>(offsetof(fmha_mxfp8_kvsplit_args, ptr_lse));
+    p.splits = ka<uint32_t>(offsetof(fmha_mxfp8_kvsplit_args, kvs_splits));
+    p.rows_total = ka<uint32_t>(offsetof(fmha_mxfp8_kvsplit_args, kvs_rows_total));
     uint32_t qt, head, z;
-    block_coords(qt, head, z);
+    block_coords(p.S, p.H, 256u, qt, head, z);
     // components.rs:20-30 / 58-74: z = batch * splits + split; split s owns tiles [s tps, min(ntiles, (s+1) tps))
     const uint32_t bidx = z / p.splits, split = z % p.splits;
     const uint32_t ntiles = (p.SK + 127u) / 128u;
@@ -715,14 +766,16 @@ extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvs
 }
 
 // epilogue.rs:89-167 / io.rs:164-185: thread t -> 8 consecutive outputs of row t >> 4 (tail threads redo the last group)
-extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvsplit_combine8h(fmha_mxfp8_combine_args a) {
-    const uint32_t rows = a.rows_total, splits = a.splits;
+extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvsplit_combine8h(fmha_mxfp8_combine_args a_) {
+    (void)a_;
+    const uint32_t rows = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, rows_total));
+    const uint32_t splits = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, splits));
     const uint32_t groups = rows << 4;
     uint32_t t = blockIdx.x * 256u + threadIdx.x;
     t = t < groups ? t : groups - 1u;
     const uint32_t row = t >> 4;
-    const float* lse = (const float*)a.ptr_lse;
-    const uint8_t* ohat = (const uint8_t*)a.ptr_ohat;
+    const float* lse = (const float*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_lse));
+    const uint8_t* ohat = (const uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_ohat));
     float m = -1.0e30f, den = 0.0f;
     float acc[8];
 #pragma unroll
@@ -750,5 +803,5 @@ extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvspli
         const v2bf w = {(__bf16)(acc[2 * i] * rd), (__bf16)(acc[2 * i + 1] * rd)};
         outv[i] = __builtin_bit_cast(int, w);
     }
-    *(v4i*)((uint8_t*)a.ptr_out + (size_t)t * 16u) = outv;
+    *(v4i*)((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u) = outv;
 }
