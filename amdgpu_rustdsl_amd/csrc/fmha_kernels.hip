@@ -79,8 +79,16 @@ struct Prm {
         if ((p).trace && (threadIdx.x & 63u) == 0u)                                                         \
             (p).trace[((size_t)(blk) * 8u + (threadIdx.x >> 6)) * 8u + (i)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
+// loop marks: shader-clock cycles at mark k of tile t (8 <= t < 24) in a second region behind the first
+#define FMHA_LMARK(p, blk, t, k)                                                                                  \
+    do {                                                                                                        \
+        if ((p).trace && (threadIdx.x & 63u) == 0u && (t) >= 8u && (t) < 24u)                                   \
+            (p).trace[65536u + ((size_t)(blk) * 8u + (threadIdx.x >> 6)) * 64u + ((t) - 8u) * 4u + (k)] =       \
+                __builtin_amdgcn_s_memtime();                                                                   \
+    } while (0)
 #else
 #define FMHA_MARK(p, blk, i) do { } while (0)
+#define FMHA_LMARK(p, blk, t, k) do { } while (0)
 #endif
 
 #define KA_AS __attribute__((address_space(4)))
@@ -455,6 +463,60 @@ struct Wave {
             }
         }
     }
+
+    // The MFMA phase of the two-group cadence as one software pipeline of 16 LDS-fed MFMAs: PV(t) (i = 0..7, V^T
+    // fragment (j, dc) = (i / 4, i % 4), plus the row sums at dc = 0) then QK(t+1) (i = 8..15, k-half c = (i - 8) / 4,
+    // accumulator t4 = (i - 8) % 4). The A operand of MFMA i is read from LDS two MFMAs ahead (a 3-deep register
+    // ring) across the PV -> QK seam, so an LDS round trip (longer than one 64-cycle MFMA under load) never stalls the
+    // matrix pipe; the Q fragments and K-scale words are read ahead the same way. `mid` runs after the first QK MFMA
+    // (the staging loads of a later tile: P and the V fragments are dead by then). A scheduling fence after every
+    // MFMA keeps the order.
+    template <bool PV, bool QK, typename Mid>
+    __device__ __forceinline__ void m_phase(uint32_t vslot, const uint32_t (&pw)[4][4], uint32_t kslot, v16f (&s)[4], Mid&& mid) {
+        const uint32_t vb = slot_base(lds, kLdsV, vslot, kTileBytes);
+        const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
+        const uint32_t ksb = slot_base(lds, kLdsKs, kslot, 512u);
+        constexpr int I0 = PV ? 0 : 8, I1 = QK ? 16 : 8;
+        auto fetch = [&](int i) -> v8i {
+            return i < 8 ? vfrag(vb, i >> 2, i & 3) : frag(kb + 4096u * (uint32_t)((i - 8) & 3), (i - 8) >> 2);
+        };
+        v8i ring[3];
+        v8i qf[2];
+        uint32_t ksw[4];
+        ring[I0 % 3] = fetch(I0);
+        if (I0 + 1 < I1) ring[(I0 + 1) % 3] = fetch(I0 + 1);
+        if (!PV && QK) {
+            qf[0] = qfrag(0);
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) ksw[t4] = kscale(ksb, t4);
+        }
+        if (QK) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[3][i] = bias;
+        }
+#pragma unroll
+        for (int i = I0; i < I1; ++i) {
+            if (i + 2 < I1) ring[(i + 2) % 3] = fetch(i + 2);
+            if (PV && QK && i == 5) {
+                qf[0] = qfrag(0);
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4) ksw[t4] = kscale(ksb, t4);
+            }
+            if (QK && i == 10) qf[1] = qfrag(1);
+            if (i < 8) {
+                const int j = i >> 2, dc = i & 3;
+                const v8i pf = pfrag(pw, j);
+                if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones_op(), pf, lacc, 0, 0, 0, 127, 0, 127);
+                o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ring[i % 3], pf, o[dc], 0, 0, 0, 127, 0, 127);
+            } else {
+                const int c = (i - 8) >> 2, t4 = (i - 8) & 3;
+                s[t4] = qk_mfma(ring[i % 3], qf[c], c == 0 ? s[3] : s[t4], ksw[t4], c);
+                if (i == 8) mid();
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (!QK) mid();
+    }
 };
 
 // The row sum of this lane's query (the ones pattern puts it in D dword (lane / 16) % 2).
@@ -571,29 +633,41 @@ __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint
         FMHA_MARK(p, tblk, 2);
         block_barrier();
         FMHA_MARK(p, tblk, 3);
-        if (w.active(key_of(0))) w.qk_all(0, s);
+        w.qk_all(0, s);
         if (grp_b) block_barrier();      // B starts one phase behind
-        for (uint32_t t = 0; t < ntiles; ++t) {
-            // ---- V(t)
+        // Every wave runs every tile of the block's range: a tile that is fully masked for a wave's rows (causal
+        // diagonal) gives P = 0 and no rebase, so the result is unchanged, and a single instantiation of the phase
+        // code keeps the register allocation spill-free.
+        auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4]) {
             __builtin_amdgcn_s_setprio(0);
             // A stores its share of tile t+1, B of tile t+2 (one uniform index: a single code path)
             const uint32_t ts = t + (grp_b ? 2u : 1u);
             if (ts < ntiles) st.store(slot_of(ts));
-            const bool act = w.active(key_of(t));
-            uint32_t pw[4][4];
-            if (act) {
-                if (w.needs_mask(key_of(t))) w.apply_mask(s, key_of(t));
-                rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
+            if (w.needs_mask(key_of(t))) w.apply_mask(s, key_of(t));
+            rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
 #pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
-            }
+            for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
+            FMHA_LMARK(p, tblk, t, 0);
             block_barrier();
-            // ---- M(t): PV(t), then (P dead) the staging loads, then QK(t+1)
+            FMHA_LMARK(p, tblk, t, 1);
             __builtin_amdgcn_s_setprio(1);
-            if (act) w.pv_all(slot_of(t), pw);
+        };
+        uint32_t t = 0;
+        for (; t + 1 < ntiles; ++t) {
+            uint32_t pw[4][4];
+            v_phase(t, pw);
+            // ---- M(t): PV(t), the staging loads of a later tile, QK(t+1)
             const uint32_t tl = t + (grp_b ? 3u : 2u);
-            st.load(key_of(tl), tl < ntiles);
-            if (t + 1 < ntiles && w.active(key_of(t + 1))) w.qk_all(slot_of(t + 1), s);
+            w.template m_phase<true, true>(slot_of(t), pw, slot_of(t + 1), s, [&] { st.load(key_of(tl), tl < ntiles); });
+            FMHA_LMARK(p, tblk, t, 2);
+            block_barrier();
+            FMHA_LMARK(p, tblk, t, 3);
+        }
+        {
+            // the last tile: PV only
+            uint32_t pw[4][4];
+            v_phase(t, pw);
+            w.template m_phase<true, false>(slot_of(t), pw, slot_of(t), s, [] {});
             block_barrier();
         }
         if (!grp_b) block_barrier();     // A ends one phase ahead: the barrier counts match
