@@ -38,8 +38,13 @@ typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 #define LDS_AS __attribute__((address_space(3)))
+#define GLOBAL_AS __attribute__((address_space(1)))
 
 namespace {
+
+#ifndef FMHA_PREFETCH
+#define FMHA_PREFETCH 2
+#endif
 
 constexpr int kD = 128;
 constexpr int kTile = 128;                    // keys per KV tile
@@ -48,8 +53,10 @@ constexpr int kSlots = 3;                     // ring depth (prefetch distance 2
 constexpr int kLdsK = 0;                      // kSlots K tiles
 constexpr int kLdsV = kSlots * kTileBytes;    // kSlots V tiles
 constexpr int kLdsQ = 2 * kSlots * kTileBytes;    // the block's Q rows (up to 256 x 128 B), swizzled like K
-constexpr int kLdsKs = kLdsQ + 256 * kD;          // kSlots x 512 B of K scales
-constexpr int kLdsBytes = kLdsKs + kSlots * 512;
+constexpr int kLdsKs = kLdsQ + 256 * kD;          // kSlots x 1 KiB of K scales: the words, then the words >> 8
+constexpr int kKsSlot = 1024;
+constexpr int kLdsKsDummy = kLdsKs + kSlots * kKsSlot;   // 1 KiB sink for the K-scale writes of threads 256..511
+constexpr int kLdsBytes = kLdsKsDummy + 1024;
 
 struct Prm {
     const uint8_t* q;
@@ -79,16 +86,26 @@ struct Prm {
         if ((p).trace && (threadIdx.x & 63u) == 0u)                                                         \
             (p).trace[((size_t)(blk) * 8u + (threadIdx.x >> 6)) * 8u + (i)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
-// loop marks: shader-clock cycles at mark k of tile t (8 <= t < 24) in a second region behind the first
+// loop marks: the shader-clock cycles between consecutive marks are summed per mark index k (k = 0..3) over tiles
+// 4 <= t < ntiles - 2 in scalar registers (no VGPRs in the loop) and written by FMHA_LFLUSH behind the first region
 #define FMHA_LMARK(p, blk, t, k)                                                                                  \
     do {                                                                                                        \
-        if ((p).trace && (threadIdx.x & 63u) == 0u && (t) >= 8u && (t) < 24u)                                   \
-            (p).trace[65536u + ((size_t)(blk) * 8u + (threadIdx.x >> 6)) * 64u + ((t) - 8u) * 4u + (k)] =       \
-                __builtin_amdgcn_s_memtime();                                                                   \
+        const uint64_t now_ = __builtin_amdgcn_s_memtime();                                                     \
+        if ((t) >= 4u && (t) + 2u < ntiles) prof_acc[k] += now_ - prof_last;                                    \
+        prof_last = now_;                                                                                       \
     } while (0)
+#define FMHA_LFLUSH(p, blk)                                                                                       \
+    do {                                                                                                        \
+        if ((p).trace && (threadIdx.x & 63u) == 0u)                                                             \
+            for (int k_ = 0; k_ < 4; ++k_)                                                                      \
+                (p).trace[65536u + ((size_t)(blk) * 8u + (threadIdx.x >> 6)) * 8u + k_] = prof_acc[k_];         \
+    } while (0)
+#define FMHA_LDECL uint64_t prof_acc[4] = {0, 0, 0, 0}; uint64_t prof_last = 0
 #else
 #define FMHA_MARK(p, blk, i) do { } while (0)
 #define FMHA_LMARK(p, blk, t, k) do { } while (0)
+#define FMHA_LFLUSH(p, blk) do { } while (0)
+#define FMHA_LDECL do { } while (0)
 #endif
 
 #define KA_AS __attribute__((address_space(4)))
@@ -180,11 +197,11 @@ struct Stager {
     static constexpr int kN = kTileBytes / (NT * 16);   // 16-byte chunks per thread per 16 KiB tile
     const uint8_t *kb, *vb, *ksb;
     uint32_t voff[kN];  // (i NT/8 + tid/8) k_seq + 16 (tid & 7)
-    uint32_t ksoff;     // tid ks_row
+    uint32_t ksoff;     // K-scale load offset: key (tid & 127) for tid < 256, out of range (zeros) beyond
+    uint32_t kswoff;    // K-scale LDS write offset in a slot (tid < 256: word tid; beyond: the sink), see store_from
+    uint32_t ksshift;   // 0 for the words (tid < 128), 8 for the shifted copies (128 <= tid < 256)
     uint32_t woff;      // (tid / 8) 128 + 16 ((tid & 7) ^ swz(tid / 8))
     uint32_t tid, k_seq, ks_row, SK, lds;
-    v4i kr[kN], vr[kN];
-    uint32_t ksr;
 
     __device__ void init(const uint8_t* kb_, const uint8_t* vb_, const uint8_t* ksb_, uint32_t k_seq_, uint32_t SK_, uint32_t lds_) {
         kb = kb_; vb = vb_; ksb = ksb_;
@@ -196,34 +213,51 @@ struct Stager {
         const uint32_t row = tid >> 3, c = tid & 7u;
 #pragma unroll
         for (int i = 0; i < kN; ++i) voff[i] = (row + (uint32_t)(i * NT / 8)) * k_seq + (c << 4);
-        ksoff = tid * ks_row;
+        ksoff = tid < 256u ? (tid & 127u) * ks_row : 0x80000000u;
+        kswoff = tid < 256u ? tid * 4u : 0u;
+        ksshift = tid < 128u ? 0u : 8u;
         woff = row * 128u + ((c ^ swz(row)) << 4);
     }
 
-    // Loads tile [key0, key0 + 128) when `valid` (zeros past SK), nothing when not.
-    __device__ __forceinline__ void load(uint32_t key0, bool valid) {
-        const uint32_t left = valid ? SK - key0 : 0u;   // keys left in the sequence from key0 (>= 1 when valid)
-        const uint32_t kvb = left ? (left - 1u) * k_seq + kD : 0u;
-        const uint32_t ksb_bytes = left ? (left - 1u) * ks_row + 4u : 0u;
+    // Loads tile [key0, key0 + 128) when `valid` (zeros past SK), nothing when not. The resource sizes are wave-uniform
+    // scalar arithmetic: rem = SK - 1 - key0 keys follow the tile's first, so the valid bytes are rem k_seq + 128.
+    struct Regs {
+        v4i kr[kN], vr[kN];
+        uint32_t ksr;
+    };
+
+    Regs cur;   // the tile staged between its load (MFMA phase) and its store (next VALU phase)
+
+    __device__ __forceinline__ void load(uint32_t key0, bool valid) { load_into(cur, key0, valid); }
+    __device__ __forceinline__ void store(uint32_t slot) const { store_from(cur, slot); }
+
+    __device__ __forceinline__ void load_into(Regs& r, uint32_t key0, bool valid) const {
+        const int rem = __builtin_amdgcn_readfirstlane((int)SK - 1 - (int)key0);
+        const uint32_t kvb = valid ? (uint32_t)max(rem * (int)k_seq + kD, 0) : 0u;
+        const uint32_t ksb_bytes = valid ? (uint32_t)max(rem * (int)ks_row + 4, 0) : 0u;
         const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb + (size_t)key0 * k_seq, kvb);
         const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + (size_t)key0 * k_seq, kvb);
         const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksb + (size_t)key0 * ks_row, ksb_bytes);
 #pragma unroll
         for (int i = 0; i < kN; ++i) {
-            kr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rk, voff[i], 0, 0));
-            vr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, voff[i], 0, 0));
+            r.kr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rk, voff[i], 0, 0));
+            r.vr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, voff[i], 0, 0));
         }
-        ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, tid < 128u ? ksoff : 0x80000000u, 0, 0);
+        r.ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, ksoff, 0, 0);
     }
 
-    __device__ __forceinline__ void store(uint32_t slot) const {
+    __device__ __forceinline__ void store_from(const Regs& r, uint32_t slot) const {
         const uint32_t kb_ = slot_base(lds, kLdsK, slot, kTileBytes) + woff, vb_ = slot_base(lds, kLdsV, slot, kTileBytes) + woff;
 #pragma unroll
         for (int i = 0; i < kN; ++i) {
-            lds_write16(kb_ + i * NT * 16, kr[i]);
-            lds_write16(vb_ + i * NT * 16, vr[i]);
+            lds_write16(kb_ + i * NT * 16, r.kr[i]);
+            lds_write16(vb_ + i * NT * 16, r.vr[i]);
         }
-        if (tid < 128u) lds_write4(slot_base(lds, kLdsKs, slot, 512u) + tid * 4u, ksr);
+        // threads 0..127: the scale word of key tid; 128..255: the word of key tid - 128 shifted down one byte (read by
+        // the lanes of the upper k-group); the rest write the sink. Unconditional, so the load is not sunk into a
+        // branch (and issued late) by the compiler.
+        const uint32_t ksw_base = tid < 256u ? slot_base(lds, kLdsKs, slot, kKsSlot) : lds + kLdsKsDummy;
+        lds_write4(ksw_base + kswoff, r.ksr >> ksshift);
     }
 };
 
@@ -231,6 +265,15 @@ struct Stager {
 // LDS operations (its tile writes become visible) but, unlike __syncthreads, not vmcnt: the staging loads of a
 // later tile stay in flight across it.
 __device__ inline void block_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// The same barrier with the wave's last N LDS operations still in flight: LDS operations complete in order, so
+// lgkmcnt(N) drains everything issued before them (the wave's tile stores) and leaves N reads issued for the next
+// phase outstanding.
+template <int N>
+__device__ inline void block_barrier_keep() {
+    static_assert(N >= 0 && N <= 15, "lgkmcnt field");
+    asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
 
 // Softmax recipe constants (softmax.rs:24-27 exact copy; softmax.rs:80-88 lazy copy).
 struct Recipe {
@@ -318,6 +361,7 @@ struct Wave {
     uint32_t kfo;      // K / Q fragment offset in a tile: row n, chunk (hh ^ swz(n)); chunk 4c + 2e + hh = kfo ^ (4c + 2e) << 4
     uint32_t vfo;      // V^T read offset: row rlo, chunk ((g & 1) ^ swz(rlo)), half pp; dim group dc = vfo ^ (2 dc) << 4
     uint32_t onew;
+    uint32_t kso;      // K-scale word offset of this lane: hh 512 + 4 n
     // causal limits: query row i sees keys [0, i + SK - S + 1) (cut to [.., key_hi))
     uint32_t lim_row, lim_wave_min, lim_wave_max, key_hi;
     // softmax state
@@ -325,9 +369,24 @@ struct Wave {
     float bias;        // b of this lane's query: the seed of every S accumulator
     v16f o[4];
     v4f lacc;
+    v4i qtmp[4];       // the lane's Q bytes between their load (init) and their LDS write (commit_q)
+    uint32_t qsw;      // the lane's Q scale word, loaded by init
 
-    // Q rows of this wave -> LDS (swizzled like a K tile, at kLdsQ + 4096 wave): the QK MFMAs read their B operand
-    // from there one k-half at a time, so only 8 Q VGPRs are live at the phase's register peak.
+    // Q rows of this wave -> LDS (commit_q), swizzled like a K tile at kLdsQ + 4096 wave, after init() issued the loads
+    __device__ __forceinline__ void commit_q() {
+        // Q scale bytes of the two k-halves (E8M0 - 9: S comes out x 2^-9)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) sq[c] = (int)(((qsw >> (8 * (2 * c + hh))) - 9u) & 0xffu);
+        const uint32_t qb = lds + kLdsQ + wave * 4096u;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) lds_write16(qb + (kfo ^ ((uint32_t)(4 * c + 2 * e) << 4)), qtmp[2 * c + e]);
+    }
+
+    // Lane constants, softmax state, and the loads of the lane's Q bytes and scales. Q goes to LDS (commit_q) rather
+    // than staying in registers: the QK MFMAs read their B operand from there one k-half at a time, so only 8 Q VGPRs
+    // are live at the phase's register peak.
     __device__ __forceinline__ void init(const Prm& p, uint32_t lds_, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_hi_) {
         lane = threadIdx.x & 63u;
         wave = wave_id();
@@ -339,19 +398,16 @@ struct Wave {
         const uint32_t row = row0 + n;
         const uint32_t row_c = min(row, p.S - 1u);
         kfo = n * 128u + ((hh ^ swz(n)) << 4);
+        kso = hh * 512u + n * 4u;
         {
             const uint8_t* qrow = p.q + (size_t)bidx * p.q_b + (size_t)row_c * p.q_seq + head * kD;
-            const uint32_t qb = lds + kLdsQ + wave * 4096u;
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int e = 0; e < 2; ++e)
-                    lds_write16(qb + (kfo ^ ((uint32_t)(4 * c + 2 * e) << 4)), *(const v4i*)(qrow + 64 * c + 32 * e + 16 * hh));
+                for (int e = 0; e < 2; ++e) qtmp[2 * c + e] = *(const GLOBAL_AS v4i*)(qrow + 64 * c + 32 * e + 16 * hh);
         }
-        const uint32_t qsw = *(const uint32_t*)(p.qs + (size_t)bidx * p.qs_b + (size_t)row_c * (p.H * 4u) + head * 4u);
-#pragma unroll
-        for (int c = 0; c < 2; ++c) sq[c] = (int)(((qsw >> (8 * (2 * c + hh))) - 9u) & 0xffu);
-        vd = *p.vd;
+        qsw = *(const GLOBAL_AS uint32_t*)(p.qs + (size_t)bidx * p.qs_b + (size_t)row_c * (p.H * 4u) + head * 4u);
+        vd = *(const GLOBAL_AS float*)p.vd;
         lim_row = lim_wave_min = lim_wave_max = key_hi;
         if (p.flags & 1u) {
             const int off = (int)p.SK - (int)p.S + 1;
@@ -395,8 +451,9 @@ struct Wave {
         return cat8(lds_read16(base + (kfo ^ ((uint32_t)(4 * c) << 4))), lds_read16(base + (kfo ^ ((uint32_t)(4 * c + 2) << 4))));
     }
     __device__ __forceinline__ v8i qfrag(int c) const { return frag(lds + kLdsQ + wave * 4096u, c); }
-    // K-scale word of 32-key block t4, shifted so op_sel byte 2c is the lane half's E8M0 byte 2c + hh
-    __device__ __forceinline__ uint32_t kscale(uint32_t ksb, int t4) const { return lds_read4(ksb + (32u * t4 + n) * 4u) >> (8u * hh); }
+    // K-scale word of 32-key block t4 for this lane's key row, read from the copy shifted down by hh bytes so that
+    // op_sel byte 2c is the lane half's E8M0 byte 2c + hh
+    __device__ __forceinline__ uint32_t kscale(uint32_t ksb, int t4) const { return lds_read4(ksb + kso + 128u * t4); }
     // V^T fragment of PV MFMA (j, dc): four transposing reads 16 keys apart
     __device__ __forceinline__ v8i vfrag(uint32_t vb, int j, int dc) const {
         const uint32_t va = vb + 8192u * j + (vfo ^ ((uint32_t)(2 * dc) << 4));
@@ -445,7 +502,7 @@ struct Wave {
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[3][i] = bias;
         const uint32_t kb = slot_base(lds, kLdsK, nslot, kTileBytes);
-        const uint32_t ksb = slot_base(lds, kLdsKs, nslot, 512u);
+        const uint32_t ksb = slot_base(lds, kLdsKs, nslot, (uint32_t)kKsSlot);
         auto kread = [&](int g) { return frag(kb + 4096u * (g & 3), g >> 2); };   // g = 4 c + t4
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -471,46 +528,74 @@ struct Wave {
     // matrix pipe; the Q fragments and K-scale words are read ahead the same way. `mid` runs after the first QK MFMA
     // (the staging loads of a later tile: P and the V fragments are dead by then). A scheduling fence after every
     // MFMA keeps the order.
+    static constexpr int DEPTH = FMHA_PREFETCH;   // MFMA-phase operand reads run DEPTH MFMAs ahead
+    typedef v8i Ring[DEPTH + 1];
+
+    // The first DEPTH V^T fragments of PV on slot `vslot`, read at the end of the VALU phase (the tile has been in LDS
+    // since before the phase began) so that the MFMA phase starts with an MFMA instead of an LDS round trip.
+    __device__ __forceinline__ void pv_prefetch(uint32_t vslot, Ring& ring) const {
+        const uint32_t vb = slot_base(lds, kLdsV, vslot, kTileBytes);
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) ring[i] = vfrag(vb, i >> 2, i & 3);
+    }
+
     template <bool PV, bool QK, typename Mid>
-    __device__ __forceinline__ void m_phase(uint32_t vslot, const uint32_t (&pw)[4][4], uint32_t kslot, v16f (&s)[4], Mid&& mid) {
+    __device__ __forceinline__ void m_phase(uint32_t vslot, const uint32_t (&pw)[4][4], uint32_t kslot, v16f (&s)[4], Ring& ring,
+                                            Mid&& mid) {
         const uint32_t vb = slot_base(lds, kLdsV, vslot, kTileBytes);
         const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
-        const uint32_t ksb = slot_base(lds, kLdsKs, kslot, 512u);
+        const uint32_t ksb = slot_base(lds, kLdsKs, kslot, (uint32_t)kKsSlot);
         constexpr int I0 = PV ? 0 : 8, I1 = QK ? 16 : 8;
+#ifdef FMHA_EXP_NO_LDS
+        // timing experiment only (wrong results): fragments read once per phase
+        const v8i fk = frag(kb, 0), fv = vfrag(vb, 0, 0);
+        auto fetch = [&](int i) -> v8i { return i < 8 ? fv : fk; };
+#else
         auto fetch = [&](int i) -> v8i {
             return i < 8 ? vfrag(vb, i >> 2, i & 3) : frag(kb + 4096u * (uint32_t)((i - 8) & 3), (i - 8) >> 2);
         };
-        v8i ring[3];
+#endif
         v8i qf[2];
         uint32_t ksw[4];
-        ring[I0 % 3] = fetch(I0);
-        if (I0 + 1 < I1) ring[(I0 + 1) % 3] = fetch(I0 + 1);
+        if (!PV) {   // with PV the caller prefetched the first fragments (pv_prefetch)
+#pragma unroll
+            for (int i = I0; i < I0 + DEPTH; ++i)
+                if (i < I1) ring[i % (DEPTH + 1)] = fetch(i);
+        }
         if (!PV && QK) {
             qf[0] = qfrag(0);
 #pragma unroll
             for (int t4 = 0; t4 < 4; ++t4) ksw[t4] = kscale(ksb, t4);
         }
-        if (QK) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[3][i] = bias;
-        }
 #pragma unroll
         for (int i = I0; i < I1; ++i) {
-            if (i + 2 < I1) ring[(i + 2) % 3] = fetch(i + 2);
-            if (PV && QK && i == 5) {
+            if (i + DEPTH < I1) ring[(i + DEPTH) % (DEPTH + 1)] = fetch(i + DEPTH);
+            if (QK && i == (PV ? 6 : I0)) {   // the seed of S (16 copies of b), just before the first QK MFMA
+#pragma unroll
+                for (int k = 0; k < 16; ++k) s[3][k] = bias;
+            }
+            if (PV && QK && i == 8 - DEPTH - 1) {
                 qf[0] = qfrag(0);
 #pragma unroll
                 for (int t4 = 0; t4 < 4; ++t4) ksw[t4] = kscale(ksb, t4);
             }
             if (QK && i == 10) qf[1] = qfrag(1);
+            // the reads above are issued before MFMA i (the scheduler would otherwise sink them past it)
+            __builtin_amdgcn_sched_barrier(0);
+#ifdef FMHA_EXP_NO_PV
+            if (i < 8) { (void)pw; } else
+#endif
+#ifdef FMHA_EXP_NO_QK
+            if (i >= 8) { (void)qf; if (i == 8) mid(); } else
+#endif
             if (i < 8) {
                 const int j = i >> 2, dc = i & 3;
                 const v8i pf = pfrag(pw, j);
                 if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones_op(), pf, lacc, 0, 0, 0, 127, 0, 127);
-                o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ring[i % 3], pf, o[dc], 0, 0, 0, 127, 0, 127);
+                o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ring[i % (DEPTH + 1)], pf, o[dc], 0, 0, 0, 127, 0, 127);
             } else {
                 const int c = (i - 8) >> 2, t4 = (i - 8) & 3;
-                s[t4] = qk_mfma(ring[i % 3], qf[c], c == 0 ? s[3] : s[t4], ksw[t4], c);
+                s[t4] = qk_mfma(ring[i % (DEPTH + 1)], qf[c], c == 0 ? s[3] : s[t4], ksw[t4], c);
                 if (i == 8) mid();
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -621,15 +706,21 @@ __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint
     auto key_of = [&](uint32_t t) { return key_lo + t * kTile; };
 
     v16f s[4];
+    FMHA_LDECL;
     if (ntiles > 0) {
-        st.load(key_of(0), true);
-        st.store(0);
-        st.load(key_of(1), ntiles > 1);
-        if (grp_b && ntiles > 1) st.store(1);
-        // in registers at the loop's entry: A its share of tile 1 (stored in V(0)), B of tile 2 (one load for both,
-        // so the staged registers have a single definition)
+        // all prologue loads in flight together (Q was issued by init): tiles 0 and 1 into prologue registers, and
+        // the tile in the staging registers at the loop's entry: A its share of tile 1 (stored in V(0)), B of tile 2
+        // (one load for both, so the staged registers have a single definition)
+        typename Stager<NT>::Regs r0, r1;
+        st.load_into(r0, key_of(0), true);
+        st.load_into(r1, key_of(1), ntiles > 1);
         const uint32_t tp = grp_b ? 2u : 1u;
         st.load(key_of(tp), tp < ntiles);
+        w.commit_q();
+        st.store_from(r0, 0);
+        // tile 1 (zeros when there is none; nobody reads slot 1 then); A stores its share again in V(0), which is
+        // harmless, and keeps the store unconditional (a conditional one gets its loads sunk into the branch)
+        st.store_from(r1, 1);
         FMHA_MARK(p, tblk, 2);
         block_barrier();
         FMHA_MARK(p, tblk, 3);
@@ -638,17 +729,27 @@ __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint
         // Every wave runs every tile of the block's range: a tile that is fully masked for a wave's rows (causal
         // diagonal) gives P = 0 and no rebase, so the result is unchanged, and a single instantiation of the phase
         // code keeps the register allocation spill-free.
+        typename Wave<NT>::Ring ring;
         auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4]) {
             __builtin_amdgcn_s_setprio(0);
             // A stores its share of tile t+1, B of tile t+2 (one uniform index: a single code path)
             const uint32_t ts = t + (grp_b ? 2u : 1u);
             if (ts < ntiles) st.store(slot_of(ts));
+#ifdef FMHA_EXP_NO_V
+            // timing experiment only (wrong results): no softmax work in the VALU phase
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+                for (int a = 0; a < 4; ++a) pw[t4][a] = __builtin_bit_cast(uint32_t, s[t4][a]);
+#else
             if (w.needs_mask(key_of(t))) w.apply_mask(s, key_of(t));
             rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
 #pragma unroll
             for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
+#endif
+            w.pv_prefetch(slot_of(t), ring);
             FMHA_LMARK(p, tblk, t, 0);
-            block_barrier();
+            block_barrier_keep<4 * Wave<NT>::DEPTH>();   // the prefetched V^T reads stay in flight
             FMHA_LMARK(p, tblk, t, 1);
             __builtin_amdgcn_s_setprio(1);
         };
@@ -658,7 +759,11 @@ __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint
             v_phase(t, pw);
             // ---- M(t): PV(t), the staging loads of a later tile, QK(t+1)
             const uint32_t tl = t + (grp_b ? 3u : 2u);
-            w.template m_phase<true, true>(slot_of(t), pw, slot_of(t + 1), s, [&] { st.load(key_of(tl), tl < ntiles); });
+#ifdef FMHA_EXP_NO_STAGE
+            w.template m_phase<true, true>(slot_of(t), pw, slot_of(t + 1), s, ring, [&] { (void)tl; });
+#else
+            w.template m_phase<true, true>(slot_of(t), pw, slot_of(t + 1), s, ring, [&] { st.load(key_of(tl), tl < ntiles); });
+#endif
             FMHA_LMARK(p, tblk, t, 2);
             block_barrier();
             FMHA_LMARK(p, tblk, t, 3);
@@ -667,13 +772,14 @@ __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint
             // the last tile: PV only
             uint32_t pw[4][4];
             v_phase(t, pw);
-            w.template m_phase<true, false>(slot_of(t), pw, slot_of(t), s, [] {});
+            w.template m_phase<true, false>(slot_of(t), pw, slot_of(t), s, ring, [] {});
             block_barrier();
         }
         if (!grp_b) block_barrier();     // A ends one phase ahead: the barrier counts match
         __builtin_amdgcn_s_setprio(0);
     }
     FMHA_MARK(p, tblk, 4);
+    FMHA_LFLUSH(p, tblk);
     epilogue<SPLIT>(p, w, head, bidx, split, rc);
     FMHA_MARK(p, tblk, 5);
 }
@@ -702,9 +808,11 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
 
     v16f s[4];
     if (ntiles > 0) {
-        st.load(key_of(0), true);
-        st.store(0);
+        typename Stager<NT>::Regs r0;
+        st.load_into(r0, key_of(0), true);
         st.load(key_of(1), ntiles > 1);
+        w.commit_q();
+        st.store_from(r0, 0);
         if (ntiles > 1) st.store(1);
         block_barrier();
         if (w.active(key_of(0))) {
@@ -722,7 +830,7 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
             if (act_next) {
                 // P(t) conversion interleaved with k-half 0 of QK(t+1) (accumulator t4 of S(t) is dead once
                 // converted; a separate seed, this path has the registers), then k-half 1
-                const uint32_t kb = slot_base(w.lds, kLdsK, nslot, kTileBytes), ksb = slot_base(w.lds, kLdsKs, nslot, 512u);
+                const uint32_t kb = slot_base(w.lds, kLdsK, nslot, kTileBytes), ksb = slot_base(w.lds, kLdsKs, nslot, (uint32_t)kKsSlot);
                 v16f seed;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) seed[i] = w.bias;
