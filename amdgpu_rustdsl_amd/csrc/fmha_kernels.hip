@@ -278,7 +278,16 @@ __device__ inline void block_barrier_keep() {
 // Softmax recipe constants (softmax.rs:24-27 exact copy; softmax.rs:80-88 lazy copy).
 struct Recipe {
     float thr, b131, conv;
+    // log2 of the mean ratio of the recipe's exp2 (the pknorm u16 read as bf16, 2^e (1 + m / 128), minus the LUT
+    // correction in the exact copy) to 2^x over uniformly distributed fractional parts: 1.037869 (no LUT) and 0.998943
+    // (LUT). P/l cancels it in O; the LSE output removes it from log2 l.
+    float exp2_bias_log2;
 };
+// the two recipe copies (softmax.rs:24-27 exact copy with the LUT; softmax.rs:80-88 lazy copy)
+__device__ inline Recipe recipe(bool lut) {
+    return lut ? Recipe{120.0f / 512.0f, 131.0f / 512.0f, 1.0f, -0.0015262115f}
+               : Recipe{__builtin_bit_cast(float, 0x3e85d086u), __builtin_bit_cast(float, 0x3e7df17eu), 0.25f, 0.0536247327f};
+}
 
 // Row max of one tile's S^T accumulators: the lane's 64 values (v_max3 chain), then the partner lane l ^ 32
 // (the other key half of the same query column) through v_permlane32_swap.
@@ -641,7 +650,8 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
         if (p.lse_out && hh == 0) {
             // natural-log LSE of the scores (extension): P = 2^(S + 512 b - 127) / conv, l = sum P
             const float hl = h2f(w.bw) + h2f(w.bw >> 16);
-            const float lse2 = l > 0.0f ? __builtin_amdgcn_logf(l) - hl * 2048.0f + 127.0f + __builtin_amdgcn_logf(rc.conv) : -INFINITY;
+            const float lse2 = l > 0.0f ? __builtin_amdgcn_logf(l) - hl * 2048.0f + 127.0f + __builtin_amdgcn_logf(rc.conv) - rc.exp2_bias_log2
+                                        : -INFINITY;
             p.lse_out[((size_t)bidx * p.H + head) * p.S + row] = lse2 * 0.69314718055994531f;
         }
     } else {
@@ -681,8 +691,7 @@ template <bool LUT, bool SPLIT>
 __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split,
                                 uint32_t key_lo, uint32_t key_hi) {
     constexpr int NT = 512;
-    const Recipe rc = LUT ? Recipe{120.0f / 512.0f, 131.0f / 512.0f, 1.0f}
-                          : Recipe{__builtin_bit_cast(float, 0x3e85d086u), __builtin_bit_cast(float, 0x3e7df17eu), 0.25f};
+    const Recipe rc = recipe(LUT);
     const uint32_t tblk = ((bidx * p.splits + split) * p.H + head) * ((p.S + 255u) / 256u) + qtile;
     (void)tblk;
     FMHA_MARK(p, tblk, 0);
@@ -792,8 +801,7 @@ template <bool LUT>
 __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_lo,
                                  uint32_t key_hi) {
     constexpr int NT = 256;
-    const Recipe rc = LUT ? Recipe{120.0f / 512.0f, 131.0f / 512.0f, 1.0f}
-                          : Recipe{__builtin_bit_cast(float, 0x3e85d086u), __builtin_bit_cast(float, 0x3e7df17eu), 0.25f};
+    const Recipe rc = recipe(LUT);
     Wave<NT> w;
     w.init(p, lds, qtile, head, bidx, key_hi);
     const uint32_t kvh = head / p.gqa;

@@ -45,3 +45,25 @@ def compare_to_emulation(out, emu, inp, rows):
     diff = np.abs(of - ef)
     return {"exact": float(np.mean(o == e)), "max_abs": float(np.nanmax(diff)) if diff.size else 0.0,
             "mean_abs": float(np.mean(diff)), "nan": int(np.isnan(of).sum())}
+
+
+def lse_reference(inp, rows):
+    """float64 natural-log LSE [B, H, rows] of the dequantised inputs (scores ln2 q.k, the kernels' base-2 convention)."""
+    dec = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy().astype(np.float64)
+    dec[[0x7F, 0xFF]] = 0.0
+    B, H, HK, S, SK = inp.B, inp.H, inp.HK, inp.S, inp.SK
+    q = dec[inp.q].reshape(B, S, H, 4, 32) * 2.0 ** (inp.qs[: B * S * H * 4].reshape(B, S, H, 4, 1).astype(np.float64) - 127)
+    k = dec[inp.k].reshape(B, SK, HK, 4, 32) * 2.0 ** (inp.ks[: B * SK * HK * 4].reshape(B, SK, HK, 4, 1).astype(np.float64) - 127)
+    q, k = q.reshape(B, S, H, D), k.reshape(B, SK, HK, D)
+    g = H // HK
+    out = np.zeros((B, H, rows))
+    for b in range(B):
+        for h in range(H):
+            s = q[b, :rows, h] @ k[b, :, h // g].T * np.log(2.0)
+            if inp.causal:
+                i = np.arange(rows)[:, None]
+                t = np.arange(SK)[None, :]
+                s = np.where(t <= i + SK - S, s, -np.inf)
+            m = s.max(1, keepdims=True)
+            out[b, h] = (m + np.log(np.exp(s - m).sum(1, keepdims=True)))[:, 0]
+    return out

@@ -60,3 +60,61 @@ def test_parity(gpu, case):
     # same recipe: element-wise closeness to the emulation (MFMA-internal summation differences only)
     assert cmp["mean_abs"] <= 0.6 * ref_stats["mean_err"], cmp
     assert cmp["max_abs"] <= 0.05, cmp
+
+
+# Extensions (no counterpart in the reference kernels): the bottom-right causal mask and the LSE output. Their bar is
+# the same statistical one against the oracle's emulation of the recipe with the mask applied (oracle.emulate honours
+# Inputs.causal; its mask is pinned against numpy in tests/test_oracle.py).
+CAUSAL_CASES = [
+    ("causal_cfg4_B2H8S2048", 2, 8, 8, 2048, 2048),
+    ("causal_ragged_B1H4S1000_SK1337", 1, 4, 4, 1000, 1337),
+    ("causal_S_gt_SK_B1H2S700_SK300", 1, 2, 2, 700, 300),   # rows with no visible key produce zeros
+    ("causal_t128_B1H2S512", 1, 2, 2, 512, 512),
+]
+
+
+@pytest.mark.parametrize("case", CAUSAL_CASES, ids=[c[0] for c in CAUSAL_CASES])
+def test_parity_causal(gpu, case):
+    name, B, H, HK, S, SK = case
+    print(f"[case] {name}", flush=True)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=True)
+    out, used, _ = gpu_util.run(inp, gpu)
+    assert used[0] in ("vs128", "t128")
+    # rows checked: all of them for the small shapes, the first 256 of every (b, h) for cfg4 (its first block,
+    # whose keys are cut by the mask on every tile of the diagonal)
+    rows = S if B * H * S * SK <= (1 << 24) else 256
+    emu = oracle.emulate(inp, rows=rows)
+    ref_stats = oracle.check_fp64(inp, emu, rows=rows)
+    stats = oracle.check_fp64(inp, out, rows=rows)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
+    print(f"[case] {name} path={used} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
+    assert not np.isnan(oracle.bf16_to_f32(out)).any()
+    assert stats["bad"] <= ref_stats["bad"]
+    assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
+    assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
+    if S > SK:
+        o = oracle.bf16_to_f32(out).reshape(B, S, H, 128)
+        assert (o[:, : S - SK] == 0).all()   # query i sees keys t <= i + SK - S: none for i < S - SK
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(1, 4, 4, 512, 640), (4, 8, 8, 1024, 1024)], ids=["t128", "vs128"])
+def test_lse_output(gpu, shape, causal):
+    """The optional natural-log LSE (kernarg 0x040): log sum_t exp(ln2 q.k_t) over the visible keys, against float64."""
+    B, H, HK, S, SK = shape
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
+    out, used, lse_t = gpu_util.run(inp, gpu, lse=True)
+    lse = lse_t.cpu().numpy()
+    ref = gpu_util.lse_reference(inp, rows=64)
+    got = lse[:, :, :64]
+    err = np.abs(got - ref)
+    print(f"[case] lse {shape} causal={causal} path={used} max_err={err.max():.3g} mean_err={err.mean():.3g}", flush=True)
+    assert np.isfinite(got).all()
+    assert used[0] == ("t128" if S == 512 else "vs128")
+    # l sums the recipe's P: an exp2 approximation (per key within a factor 1.087 of 2^x, bias removed on average) then
+    # e4m3 rounding. A row with few visible keys (causal, top rows) keeps its keys' approximation error, up to
+    # ln 1.087 = 0.083; over many keys it averages out to a few 1e-3.
+    assert err.max() < 0.09
+    nvis = np.minimum(SK, np.arange(64) + SK - S + 1) if causal else np.full(64, SK)
+    many = nvis >= 64
+    assert err[:, :, many].mean() < 4e-3
