@@ -132,7 +132,7 @@ int get_functions(hipFunction_t** out, char* err, size_t errlen) {
                 e = hipModuleGetFunction(&dm.fn[i], mod, kKernelNames[i]);
                 if (e != hipSuccess) {
                     set_err(err, errlen, "hipModuleGetFunction(%s): %s", kKernelNames[i], hipGetErrorString(e));
-                    hipModuleUnload(mod);
+                    (void)hipModuleUnload(mod);
                     return FMHA_ERR_NO_DEVICE;
                 }
             }
