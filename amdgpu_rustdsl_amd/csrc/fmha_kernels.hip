@@ -24,6 +24,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+#include <type_traits>
 #include <stdint.h>
 
 #include "../../include/fmha_mxfp8.h"
@@ -167,6 +168,13 @@ __device__ inline v2i lds_read_tr8(uint32_t off) { return __builtin_amdgcn_ds_re
 
 __device__ inline v8i cat8(v4i a, v4i b) { return (v8i){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}; }
 
+__device__ inline const uint8_t* uniform_ptr(const uint8_t* p) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 // Buffer resource over [base, base + bytes): the staging loads are range-checked by the hardware (an
 // out-of-range lane reads zeros) on top of the explicit key clamp of the last tile. The base and size are
 // wave-uniform by construction; readfirstlane states it so the resource lives in SGPRs (a resource the compiler
@@ -204,7 +212,8 @@ struct Stager {
     uint32_t tid, k_seq, ks_row, SK, lds;
 
     __device__ void init(const uint8_t* kb_, const uint8_t* vb_, const uint8_t* ksb_, uint32_t k_seq_, uint32_t SK_, uint32_t lds_) {
-        kb = kb_; vb = vb_; ksb = ksb_;
+        // wave-uniform base pointers (readfirstlane states it), so the per-tile resource arithmetic stays scalar
+        kb = uniform_ptr(kb_); vb = uniform_ptr(vb_); ksb = uniform_ptr(ksb_);
         tid = threadIdx.x;
         k_seq = k_seq_;
         ks_row = k_seq_ >> 5;
@@ -228,16 +237,23 @@ struct Stager {
 
     Regs cur;   // the tile staged between its load (MFMA phase) and its store (next VALU phase)
 
-    __device__ __forceinline__ void load(uint32_t key0, bool valid) { load_into(cur, key0, valid); }
-    __device__ __forceinline__ void store(uint32_t slot) const { store_from(cur, slot); }
+    // Loads this thread's share of K tile [kkey0, kkey0 + 128) (with its scales) and of V tile [vkey0, vkey0 + 128);
+    // a part that is not valid reads zeros and no memory.
+    __device__ __forceinline__ void load(uint32_t kkey0, bool kvalid, uint32_t vkey0, bool vvalid) {
+        load_into(cur, kkey0, kvalid, vkey0, vvalid);
+    }
+    __device__ __forceinline__ void store(uint32_t kslot, uint32_t vslot) const { store_from(cur, kslot, vslot); }
 
-    __device__ __forceinline__ void load_into(Regs& r, uint32_t key0, bool valid) const {
+    // resource size of a tile starting at key0: rem = SK - 1 - key0 keys follow the first, rem stride + tail bytes
+    __device__ __forceinline__ uint32_t tile_bytes(uint32_t key0, bool valid, uint32_t stride, int tail) const {
         const int rem = __builtin_amdgcn_readfirstlane((int)SK - 1 - (int)key0);
-        const uint32_t kvb = valid ? (uint32_t)max(rem * (int)k_seq + kD, 0) : 0u;
-        const uint32_t ksb_bytes = valid ? (uint32_t)max(rem * (int)ks_row + 4, 0) : 0u;
-        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb + (size_t)key0 * k_seq, kvb);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + (size_t)key0 * k_seq, kvb);
-        const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksb + (size_t)key0 * ks_row, ksb_bytes);
+        return valid ? (uint32_t)max(rem * (int)stride + tail, 0) : 0u;
+    }
+
+    __device__ __forceinline__ void load_into(Regs& r, uint32_t kkey0, bool kvalid, uint32_t vkey0, bool vvalid) const {
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb + (size_t)kkey0 * k_seq, tile_bytes(kkey0, kvalid, k_seq, kD));
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + (size_t)vkey0 * k_seq, tile_bytes(vkey0, vvalid, k_seq, kD));
+        const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksb + (size_t)kkey0 * ks_row, tile_bytes(kkey0, kvalid, ks_row, 4));
 #pragma unroll
         for (int i = 0; i < kN; ++i) {
             r.kr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rk, voff[i], 0, 0));
@@ -246,8 +262,8 @@ struct Stager {
         r.ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, ksoff, 0, 0);
     }
 
-    __device__ __forceinline__ void store_from(const Regs& r, uint32_t slot) const {
-        const uint32_t kb_ = slot_base(lds, kLdsK, slot, kTileBytes) + woff, vb_ = slot_base(lds, kLdsV, slot, kTileBytes) + woff;
+    __device__ __forceinline__ void store_from(const Regs& r, uint32_t kslot, uint32_t vslot) const {
+        const uint32_t kb_ = slot_base(lds, kLdsK, kslot, kTileBytes) + woff, vb_ = slot_base(lds, kLdsV, vslot, kTileBytes) + woff;
 #pragma unroll
         for (int i = 0; i < kN; ++i) {
             lds_write16(kb_ + i * NT * 16, r.kr[i]);
@@ -256,7 +272,7 @@ struct Stager {
         // threads 0..127: the scale word of key tid; 128..255: the word of key tid - 128 shifted down one byte (read by
         // the lanes of the upper k-group); the rest write the sink. Unconditional, so the load is not sunk into a
         // branch (and issued late) by the compiler.
-        const uint32_t ksw_base = tid < 256u ? slot_base(lds, kLdsKs, slot, kKsSlot) : lds + kLdsKsDummy;
+        const uint32_t ksw_base = tid < 256u ? slot_base(lds, kLdsKs, kslot, kKsSlot) : lds + kLdsKsDummy;
         lds_write4(ksw_base + kswoff, r.ksr >> ksshift);
     }
 };
@@ -272,8 +288,17 @@ __device__ inline void block_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts
 template <int N>
 __device__ inline void block_barrier_keep() {
     static_assert(N >= 0 && N <= 15, "lgkmcnt field");
+#ifdef FMHA_EXP_NO_LOOP_BARRIER
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");   // timing experiment only (races)
+#else
     asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+#endif
 }
+#ifdef FMHA_EXP_NO_LOOP_BARRIER
+__device__ inline void loop_barrier() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+#else
+__device__ inline void loop_barrier() { block_barrier(); }
+#endif
 
 // Softmax recipe constants (softmax.rs:24-27 exact copy; softmax.rs:80-88 lazy copy).
 struct Recipe {
@@ -350,7 +375,9 @@ __device__ __forceinline__ void convert_p(const Recipe& rc, const v16f& s, uint3
             u01 = u01 - __builtin_bit_cast(v2u16, __builtin_amdgcn_perm(0x03070a0bu, 0x0b090600u, i01));
             u23 = u23 - __builtin_bit_cast(v2u16, __builtin_amdgcn_perm(0x03070a0bu, 0x0b090600u, i23));
         }
-        v2s w = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16((v2s){0, 0}, __builtin_bit_cast(v2bf, u01), rc.conv, false);
+        // the first conversion writes the low half-word; its "old" operand (whose high half survives until the second
+        // conversion overwrites it) is the dead u01 register, so the destination needs no zero-initialisation
+        v2s w = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(__builtin_bit_cast(v2s, u01), __builtin_bit_cast(v2bf, u01), rc.conv, false);
         w = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(w, __builtin_bit_cast(v2bf, u23), rc.conv, true);
         pw[a] = __builtin_bit_cast(uint32_t, w);
     }
@@ -566,6 +593,8 @@ struct Wave {
 #endif
         v8i qf[2];
         uint32_t ksw[4];
+        v8i ones;
+        if (PV) ones = ones_op();   // once per tile for both row-sum MFMAs
         if (!PV) {   // with PV the caller prefetched the first fragments (pv_prefetch)
 #pragma unroll
             for (int i = I0; i < I0 + DEPTH; ++i)
@@ -600,7 +629,7 @@ struct Wave {
             if (i < 8) {
                 const int j = i >> 2, dc = i & 3;
                 const v8i pf = pfrag(pw, j);
-                if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones_op(), pf, lacc, 0, 0, 0, 127, 0, 127);
+                if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, pf, lacc, 0, 0, 0, 127, 0, 127);
                 o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ring[i % (DEPTH + 1)], pf, o[dc], 0, 0, 0, 127, 0, 127);
             } else {
                 const int c = (i - 8) >> 2, t4 = (i - 8) & 3;
@@ -687,9 +716,9 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
 // B M(t-1); f = 2t + 1: A M(t), B V(t). Tile u's slot (u % 3) is read in phases 2u-1 .. 2u+2 and must be written
 // before 2u-1: A writes its share of tile t+1 in V(t) (loaded in M(t-1)), B its share of tile t+2 in V(t)
 // (loaded in M(t-1)); every write lands in a slot whose last read phase has passed.
-template <bool LUT, bool SPLIT>
-__device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split,
-                                uint32_t key_lo, uint32_t key_hi) {
+template <bool LUT, bool SPLIT, bool GB>
+__device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx,
+                                                      uint32_t split, uint32_t key_lo, uint32_t key_hi) {
     constexpr int NT = 512;
     const Recipe rc = recipe(LUT);
     const uint32_t tblk = ((bidx * p.splits + split) * p.H + head) * ((p.S + 255u) / 256u) + qtile;
@@ -701,7 +730,6 @@ __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint
     Wave<NT> w;
     w.init(p, lds, qtile, head, bidx, key_hi);
     FMHA_MARK(p, tblk, 1);
-    const bool grp_b = w.wave >= 4u;
     const uint32_t kvh = head / p.gqa;
     const bool causal = (p.flags & 1u) != 0;
     uint32_t key_end = key_hi;   // the block's last useful key + 1
@@ -717,80 +745,93 @@ __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint
     v16f s[4];
     FMHA_LDECL;
     if (ntiles > 0) {
-        // all prologue loads in flight together (Q was issued by init): tiles 0 and 1 into prologue registers, and
-        // the tile in the staging registers at the loop's entry: A its share of tile 1 (stored in V(0)), B of tile 2
-        // (one load for both, so the staged registers have a single definition)
+        // One barrier per tile. Group A (waves 0-3) runs  V(t) | barrier | M(t),  group B (waves 4-7)  V(t) M(t) |
+        // barrier, so between barriers t-1 and t, A runs M(t-1) then V(t) while B runs V(t) then M(t): each SIMD
+        // holds one wave of each group, and one converts while the other multiplies without a barrier in between.
+        // Staging: V(t) stores the wave's share of K tile t+2 (with its scales) and of V tile t+1, then loads K t+3
+        // and V t+2 (a full iteration ahead of their store). In the interval before barrier t the reads touch K slots
+        // t, t+1 and V slots t-1, t, the writes K slot t+2 and V slot t+1 (mod 3): disjoint, and every read tile was
+        // written before the previous barrier.
         typename Stager<NT>::Regs r0, r1;
-        st.load_into(r0, key_of(0), true);
-        st.load_into(r1, key_of(1), ntiles > 1);
-        const uint32_t tp = grp_b ? 2u : 1u;
-        st.load(key_of(tp), tp < ntiles);
+        st.load_into(r0, key_of(0), true, key_of(0), true);            // K 0, V 0
+        st.load_into(r1, key_of(1), ntiles > 1, key_of(2), false);     // K 1 (its V part: zeros into V slot 2)
+        st.load(key_of(2), ntiles > 2, key_of(1), ntiles > 1);         // K 2, V 1: stored in V(0)
         w.commit_q();
-        st.store_from(r0, 0);
-        // tile 1 (zeros when there is none; nobody reads slot 1 then); A stores its share again in V(0), which is
-        // harmless, and keeps the store unconditional (a conditional one gets its loads sunk into the branch)
-        st.store_from(r1, 1);
+        st.store_from(r0, 0, 0);
+        st.store_from(r1, 1, 2);
         FMHA_MARK(p, tblk, 2);
         block_barrier();
         FMHA_MARK(p, tblk, 3);
         w.qk_all(0, s);
-        if (grp_b) block_barrier();      // B starts one phase behind
         // Every wave runs every tile of the block's range: a tile that is fully masked for a wave's rows (causal
         // diagonal) gives P = 0 and no rebase, so the result is unchanged, and a single instantiation of the phase
         // code keeps the register allocation spill-free.
-        typename Wave<NT>::Ring ring;
-        auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4]) {
-            __builtin_amdgcn_s_setprio(0);
-            // A stores its share of tile t+1, B of tile t+2 (one uniform index: a single code path)
-            const uint32_t ts = t + (grp_b ? 2u : 1u);
-            if (ts < ntiles) st.store(slot_of(ts));
-#ifdef FMHA_EXP_NO_V
-            // timing experiment only (wrong results): no softmax work in the VALU phase
-#pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4)
-#pragma unroll
-                for (int a = 0; a < 4; ++a) pw[t4][a] = __builtin_bit_cast(uint32_t, s[t4][a]);
-#else
-            if (w.needs_mask(key_of(t))) w.apply_mask(s, key_of(t));
-            rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
-#pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
-#endif
-            w.pv_prefetch(slot_of(t), ring);
-            FMHA_LMARK(p, tblk, t, 0);
-            block_barrier_keep<4 * Wave<NT>::DEPTH>();   // the prefetched V^T reads stay in flight
-            FMHA_LMARK(p, tblk, t, 1);
-            __builtin_amdgcn_s_setprio(1);
-        };
-        uint32_t t = 0;
-        for (; t + 1 < ntiles; ++t) {
-            uint32_t pw[4][4];
-            v_phase(t, pw);
-            // ---- M(t): PV(t), the staging loads of a later tile, QK(t+1)
-            const uint32_t tl = t + (grp_b ? 3u : 2u);
-#ifdef FMHA_EXP_NO_STAGE
-            w.template m_phase<true, true>(slot_of(t), pw, slot_of(t + 1), s, ring, [&] { (void)tl; });
-#else
-            w.template m_phase<true, true>(slot_of(t), pw, slot_of(t + 1), s, ring, [&] { st.load(key_of(tl), tl < ntiles); });
-#endif
-            FMHA_LMARK(p, tblk, t, 2);
-            block_barrier();
-            FMHA_LMARK(p, tblk, t, 3);
-        }
         {
-            // the last tile: PV only
-            uint32_t pw[4][4];
-            v_phase(t, pw);
-            w.template m_phase<true, false>(slot_of(t), pw, slot_of(t), s, ring, [] {});
-            block_barrier();
+            typename Wave<NT>::Ring ring;
+            auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4]) {
+                __builtin_amdgcn_s_setprio(0);
+                st.store(slot_of(t + 2), slot_of(t + 1));   // zeros past the range: those slots are never read again
+                // the next staging loads (K t+3, V t+2) right behind the stores: a full iteration of latency cover
+                st.load(key_of(t + 3), t + 3 < ntiles, key_of(t + 2), t + 2 < ntiles);
+#ifdef FMHA_EXP_NO_V
+                // timing experiment only (wrong results): no softmax work in the VALU phase
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+                    for (int a = 0; a < 4; ++a) pw[t4][a] = __builtin_bit_cast(uint32_t, s[t4][a]);
+#else
+                if (w.needs_mask(key_of(t))) w.apply_mask(s, key_of(t));
+                rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
+#endif
+                w.pv_prefetch(slot_of(t), ring);
+                FMHA_LMARK(p, tblk, t, 0);
+                if (!GB) block_barrier_keep<4 * Wave<NT>::DEPTH>();   // A: the prefetched V^T reads stay in flight
+                // B: a compiler-only memory fence where A has its barrier. Without one, the loop-invariant Q-fragment
+                // LDS reads get hoisted out of the loop and their registers stay live throughout (spills).
+                if (GB) asm volatile("" ::: "memory");
+                FMHA_LMARK(p, tblk, t, 1);
+                __builtin_amdgcn_s_setprio(1);
+            };
+            uint32_t t = 0;
+            for (; t + 1 < ntiles; ++t) {
+                uint32_t pw[4][4];
+                v_phase(t, pw);
+                w.template m_phase<true, true>(slot_of(t), pw, slot_of(t + 1), s, ring, [] {});
+                FMHA_LMARK(p, tblk, t, 2);
+                if (GB) loop_barrier();
+                else asm volatile("" ::: "memory");   // A: the compiler-only fence where B has its barrier
+                FMHA_LMARK(p, tblk, t, 3);
+            }
+            {
+                // the last tile: PV only
+                uint32_t pw[4][4];
+                v_phase(t, pw);
+                w.template m_phase<true, false>(slot_of(t), pw, slot_of(t), s, ring, [] {});
+                if (GB) block_barrier();
+            }
         }
-        if (!grp_b) block_barrier();     // A ends one phase ahead: the barrier counts match
         __builtin_amdgcn_s_setprio(0);
     }
     FMHA_MARK(p, tblk, 4);
     FMHA_LFLUSH(p, tblk);
     epilogue<SPLIT>(p, w, head, bidx, split, rc);
     FMHA_MARK(p, tblk, 5);
+}
+
+// The whole routine is instantiated per group (the groups place their barrier differently; one body with a
+// group-dependent branch, or two loop copies sharing a prologue, made the register allocation spill).
+template <bool LUT, bool SPLIT>
+__device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split,
+                                uint32_t key_lo, uint32_t key_hi) {
+#ifndef FMHA_LOCKSTEP
+    if (wave_id() >= 4u) attend_pingpong_group<LUT, SPLIT, true>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
+    else attend_pingpong_group<LUT, SPLIT, false>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
+#else
+    // measurement variant: all eight waves in lockstep (V | barrier | M); the slot schedule is race-free either way
+    attend_pingpong_group<LUT, SPLIT, false>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
+#endif
 }
 
 // One 4-wave group (_t128: one wave per SIMD, so each wave overlaps its own VALU with its own MFMAs): S(t) is
@@ -817,11 +858,11 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
     v16f s[4];
     if (ntiles > 0) {
         typename Stager<NT>::Regs r0;
-        st.load_into(r0, key_of(0), true);
-        st.load(key_of(1), ntiles > 1);
+        st.load_into(r0, key_of(0), true, key_of(0), true);
+        st.load(key_of(1), ntiles > 1, key_of(1), ntiles > 1);
         w.commit_q();
-        st.store_from(r0, 0);
-        if (ntiles > 1) st.store(1);
+        st.store_from(r0, 0, 0);
+        if (ntiles > 1) st.store(1, 1);
         block_barrier();
         if (w.active(key_of(0))) {
             w.qk_all(0, s);
@@ -832,7 +873,7 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
         for (uint32_t t = 0; t + 1 < ntiles; ++t) {
             const uint32_t nslot = slot == 2u ? 0u : slot + 1u;
             const uint32_t sslot = nslot == 2u ? 0u : nslot + 1u;   // slot of tile t+2
-            st.load(key_of(t + 2), t + 2 < ntiles);
+            st.load(key_of(t + 2), t + 2 < ntiles, key_of(t + 2), t + 2 < ntiles);
             const bool act = w.active(key_of(t)), act_next = w.active(key_of(t + 1));
             uint32_t pw[4][4];
             if (act_next) {
@@ -861,7 +902,7 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
                 if (w.needs_mask(key_of(t + 1))) w.apply_mask(s, key_of(t + 1));
                 m = row_max(s);
             }
-            if (t + 2 < ntiles) st.store(sslot);
+            if (t + 2 < ntiles) st.store(sslot, sslot);
             block_barrier();
             if (act_next) rebase<LUT>(rc, m, s, w.o, w.lacc, w.bias, w.bw);
             slot = nslot;
