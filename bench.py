@@ -66,8 +66,9 @@ def cpu_baseline(B, H, HK, S, SK, causal, budget_s=12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=100)
+    # the GPU clock ramps for several milliseconds under this load: 1000 warm-up steps (~40 ms) reach the steady clock
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
@@ -132,6 +133,7 @@ def main():
     ms_events = e0.elapsed_time(e1) / args.steps
     ms_wall = wall * 1e3 / args.steps
     ms = max(ms_events, ms_wall)
+    print(f"bench: {args.steps} steps, events {ms_events * 1e3:.2f} us/step, wall {ms_wall * 1e3:.2f} us/step", file=sys.stderr)
     fl = flops_of(B, H, S, SK, causal)
     tflops = fl / (ms * 1e-3) / 1e12
 
