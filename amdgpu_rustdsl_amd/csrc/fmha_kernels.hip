@@ -39,6 +39,12 @@ typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 #define LDS_AS __attribute__((address_space(3)))
+// wave issue priority around the MFMA phases (measurement builds can turn it off)
+#ifdef FMHA_NO_SETPRIO
+#define FMHA_SETPRIO(x) do { } while (0)
+#else
+#define FMHA_SETPRIO(x) __builtin_amdgcn_s_setprio(x)
+#endif
 #define GLOBAL_AS __attribute__((address_space(1)))
 
 namespace {
@@ -769,7 +775,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
         {
             typename Wave<NT>::Ring ring;
             auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4]) {
-                __builtin_amdgcn_s_setprio(0);
+                FMHA_SETPRIO(0);
                 st.store(slot_of(t + 2), slot_of(t + 1));   // zeros past the range: those slots are never read again
                 // the next staging loads (K t+3, V t+2) right behind the stores: a full iteration of latency cover
                 st.load(key_of(t + 3), t + 3 < ntiles, key_of(t + 2), t + 2 < ntiles);
@@ -792,7 +798,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
                 // LDS reads get hoisted out of the loop and their registers stay live throughout (spills).
                 if (GB) asm volatile("" ::: "memory");
                 FMHA_LMARK(p, tblk, t, 1);
-                __builtin_amdgcn_s_setprio(1);
+                FMHA_SETPRIO(1);
             };
             uint32_t t = 0;
             for (; t + 1 < ntiles; ++t) {
@@ -812,7 +818,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
                 if (GB) block_barrier();
             }
         }
-        __builtin_amdgcn_s_setprio(0);
+        FMHA_SETPRIO(0);
     }
     FMHA_MARK(p, tblk, 4);
     FMHA_LFLUSH(p, tblk);
