@@ -167,11 +167,22 @@ __device__ inline uint32_t slot_base(uint32_t lds, uint32_t region, uint32_t slo
     return __builtin_amdgcn_readfirstlane(lds + region + slot * slot_bytes);
 }
 
+// uniform base + per-lane offset as one opaque VGPR: constant offsets added to it afterwards fold into the LDS
+// instruction's immediate (left to itself the compiler reassociates base + constant first, one add per read)
+__device__ inline uint32_t lane_addr(uint32_t uniform_base, uint32_t lane_off) {
+    uint32_t r;
+    asm("v_add_u32 %0, %1, %2" : "=v"(r) : "s"(uniform_base), "v"(lane_off));
+    return r;
+}
+
 __device__ inline v4i lds_read16(uint32_t off) { return *(const LDS_AS v4i*)(uintptr_t)off; }
 __device__ inline uint32_t lds_read4(uint32_t off) { return *(const LDS_AS uint32_t*)(uintptr_t)off; }
 
 __device__ inline v2i lds_read_tr8(uint32_t off) { return __builtin_amdgcn_ds_read_tr8_b64_v2i32((LDS_AS v2i*)(uintptr_t)off); }
 
+typedef float v8f __attribute__((ext_vector_type(8)));
+__device__ inline v8f splat8(float x) { return (v8f){x, x, x, x, x, x, x, x}; }
+__device__ inline v16f splat16(float x) { return (v16f){x, x, x, x, x, x, x, x, x, x, x, x, x, x, x, x}; }
 __device__ inline v8i cat8(v4i a, v4i b) { return (v8i){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}; }
 
 __device__ inline const uint8_t* uniform_ptr(const uint8_t* p) {
@@ -489,16 +500,19 @@ struct Wave {
     }
 
     // 32-byte K or Q fragment of k-half c (c = 0: d 0..63, 1: d 64..127) of row n of the tile at `base`
-    __device__ __forceinline__ v8i frag(uint32_t base, int c) const {
-        return cat8(lds_read16(base + (kfo ^ ((uint32_t)(4 * c) << 4))), lds_read16(base + (kfo ^ ((uint32_t)(4 * c + 2) << 4))));
+    // (The slot base is added to the lane offset first and the 4 KiB block offset last, so the block offset folds into
+    // the instruction's immediate: one address add per lane-offset variant and tile instead of one per read.)
+    __device__ __forceinline__ v8i frag(uint32_t base, int c, uint32_t block_off = 0) const {
+        return cat8(lds_read16(lane_addr(base, kfo ^ ((uint32_t)(4 * c) << 4)) + block_off),
+                    lds_read16(lane_addr(base, kfo ^ ((uint32_t)(4 * c + 2) << 4)) + block_off));
     }
     __device__ __forceinline__ v8i qfrag(int c) const { return frag(lds + kLdsQ + wave * 4096u, c); }
     // K-scale word of 32-key block t4 for this lane's key row, read from the copy shifted down by hh bytes so that
     // op_sel byte 2c is the lane half's E8M0 byte 2c + hh
-    __device__ __forceinline__ uint32_t kscale(uint32_t ksb, int t4) const { return lds_read4(ksb + kso + 128u * t4); }
+    __device__ __forceinline__ uint32_t kscale(uint32_t ksb, int t4) const { return lds_read4(lane_addr(ksb, kso) + 128u * t4); }
     // V^T fragment of PV MFMA (j, dc): four transposing reads 16 keys apart
     __device__ __forceinline__ v8i vfrag(uint32_t vb, int j, int dc) const {
-        const uint32_t va = vb + 8192u * j + (vfo ^ ((uint32_t)(2 * dc) << 4));
+        const uint32_t va = lane_addr(vb, vfo ^ ((uint32_t)(2 * dc) << 4)) + 8192u * j;
         const v2i r0 = lds_read_tr8(va), r1 = lds_read_tr8(va + 2048u), r2 = lds_read_tr8(va + 4096u), r3 = lds_read_tr8(va + 6144u);
         return (v8i){r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
     }
@@ -511,7 +525,7 @@ struct Wave {
     __device__ __forceinline__ v8i ones_op() const {
         uint32_t x;
         asm volatile("v_mov_b32 %0, %1" : "=v"(x) : "v"(onew));
-        return (v8i){(int)x, (int)x, (int)x, (int)x, (int)x, (int)x, (int)x, (int)x};
+        return __builtin_bit_cast(v8i, splat8(__builtin_bit_cast(float, x)));
     }
     __device__ __forceinline__ v16f qk_mfma(const v8i& kf, const v8i& qf, const v16f& c_in, uint32_t ksw, int c) const {
         // scaled fp8 MFMA: A = K (rows = keys), B = Q^T (columns = queries), E8M0 scales per 32 of k
@@ -545,7 +559,7 @@ struct Wave {
         for (int i = 0; i < 16; ++i) s[3][i] = bias;
         const uint32_t kb = slot_base(lds, kLdsK, nslot, kTileBytes);
         const uint32_t ksb = slot_base(lds, kLdsKs, nslot, (uint32_t)kKsSlot);
-        auto kread = [&](int g) { return frag(kb + 4096u * (g & 3), g >> 2); };   // g = 4 c + t4
+        auto kread = [&](int g) { return frag(kb, g >> 2, 4096u * (g & 3)); };   // g = 4 c + t4
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const v8i qf = qfrag(c);
@@ -594,7 +608,7 @@ struct Wave {
         auto fetch = [&](int i) -> v8i { return i < 8 ? fv : fk; };
 #else
         auto fetch = [&](int i) -> v8i {
-            return i < 8 ? vfrag(vb, i >> 2, i & 3) : frag(kb + 4096u * (uint32_t)((i - 8) & 3), (i - 8) >> 2);
+            return i < 8 ? vfrag(vb, i >> 2, i & 3) : frag(kb, (i - 8) >> 2, 4096u * (uint32_t)((i - 8) & 3));
         };
 #endif
         v8i qf[2];
@@ -614,10 +628,7 @@ struct Wave {
 #pragma unroll
         for (int i = I0; i < I1; ++i) {
             if (i + DEPTH < I1) ring[(i + DEPTH) % (DEPTH + 1)] = fetch(i + DEPTH);
-            if (QK && i == (PV ? 6 : I0)) {   // the seed of S (16 copies of b), just before the first QK MFMA
-#pragma unroll
-                for (int k = 0; k < 16; ++k) s[3][k] = bias;
-            }
+            if (QK && i == (PV ? 6 : I0)) s[3] = splat16(bias);   // the seed of S (16 copies of b), before the first QK MFMA
             if (PV && QK && i == 8 - DEPTH - 1) {
                 qf[0] = qfrag(0);
 #pragma unroll
@@ -893,11 +904,11 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
 #pragma unroll
                 for (int t4 = 0; t4 < 4; ++t4) {
                     convert_p<LUT>(rc, s[t4], pw[t4]);
-                    s[t4] = w.qk_mfma(w.frag(kb + 4096u * t4, 0), q0, seed, w.kscale(ksb, t4), 0);
+                    s[t4] = w.qk_mfma(w.frag(kb, 0, 4096u * t4), q0, seed, w.kscale(ksb, t4), 0);
                 }
                 const v8i q1 = w.qfrag(1);
 #pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) s[t4] = w.qk_mfma(w.frag(kb + 4096u * t4, 1), q1, s[t4], w.kscale(ksb, t4), 1);
+                for (int t4 = 0; t4 < 4; ++t4) s[t4] = w.qk_mfma(w.frag(kb, 1, 4096u * t4), q1, s[t4], w.kscale(ksb, t4), 1);
             } else if (act) {
 #pragma unroll
                 for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
