@@ -3,8 +3,10 @@
     python -m amdgpu_rustdsl_amd.build          # or __graft_entry__.build()
 
 Outputs (in-tree, git-ignored, shipped with the source tree):
-    amdgpu_rustdsl_amd/_build/fmha_mxfp8_gfx950.hsaco   the four kernels (hipcc --genco, gfx950 only)
-    amdgpu_rustdsl_amd/_build/libfmha_mxfp8.so          include/fmha_mxfp8.h, code object embedded
+    amdgpu_rustdsl_amd/_build/fmha_mxfp8_gfx950.hsaco   the four FMHA kernels (hipcc --genco, gfx950 only)
+    amdgpu_rustdsl_amd/_build/mxfp8_quant_gfx950.hsaco  the quantisers
+    amdgpu_rustdsl_amd/_build/libfmha_mxfp8.so          include/fmha_mxfp8.h + include/mxfp8_quant.h, both code
+                                                        objects embedded
 """
 import os
 import subprocess
@@ -16,6 +18,7 @@ CSRC = os.path.join(PKG, "csrc")
 OUT = os.path.join(PKG, "_build")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HSACO = os.path.join(OUT, "fmha_mxfp8_gfx950.hsaco")
+QHSACO = os.path.join(OUT, "mxfp8_quant_gfx950.hsaco")
 LIB = os.path.join(OUT, "libfmha_mxfp8.so")
 
 # Packed FP32 VALU forms are kept out of the kernels (their results have been unreliable on this hardware pool);
@@ -36,9 +39,10 @@ def build(verbose=False):
     os.makedirs(OUT, exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     _run([hipcc, *HIP_FLAGS, "--genco", os.path.join(CSRC, "fmha_kernels.hip"), "-o", HSACO])
+    _run([hipcc, *HIP_FLAGS, "--genco", os.path.join(CSRC, "quant_kernels.hip"), "-o", QHSACO])
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
-          "-I" + os.path.join(ROCM, "include"), '-DFMHA_HSACO_PATH="%s"' % HSACO,
-          os.path.join(CSRC, "fmha_host.cpp"), "-L" + os.path.join(ROCM, "lib"), "-lamdhip64",
+          "-I" + os.path.join(ROCM, "include"), '-DFMHA_HSACO_PATH="%s"' % HSACO, '-DMXQ_HSACO_PATH="%s"' % QHSACO,
+          os.path.join(CSRC, "fmha_host.cpp"), os.path.join(CSRC, "quant_host.cpp"), "-L" + os.path.join(ROCM, "lib"), "-lamdhip64",
           "-Wl,-rpath," + os.path.join(ROCM, "lib"), "-o", LIB])
     if verbose:
         print("built", HSACO, os.path.getsize(HSACO), "bytes;", LIB, os.path.getsize(LIB), "bytes")

@@ -8,14 +8,11 @@
 
 #include <hip/hip_runtime.h>
 
-#include <cstdarg>
 #include <cstdint>
-#include <cstdio>
-#include <atomic>
 #include <cstring>
-#include <mutex>
 
 #include "../../include/fmha_mxfp8.h"
+#include "module_cache.h"
 
 static_assert(sizeof(fmha_mxfp8_args) == 656, "kernarg size (vs128_abi.h:126)");
 static_assert(offsetof(fmha_mxfp8_args, ptr_o) == 0x000, "ptr_o");
@@ -75,7 +72,9 @@ extern "C" const unsigned char fmha_mxfp8_hsaco_end[];
 
 namespace {
 
-constexpr int kMaxDevices = 64;
+using fmha_internal::fail;
+using fmha_internal::set_err;
+
 const char* const kKernelNames[4] = {
     "fmha_fwd_hd128_mxfp8_v3_vs128",
     "fmha_fwd_hd128_mxfp8_v3_t128",
@@ -84,80 +83,13 @@ const char* const kKernelNames[4] = {
 };
 enum { K_VS128 = 0, K_T128 = 1, K_KVSPLIT = 2, K_COMBINE = 3 };
 
-struct DeviceModule {
-    std::atomic<bool> loaded{false};
-    hipModule_t mod = nullptr;
-    hipFunction_t fn[4] = {nullptr, nullptr, nullptr, nullptr};
-};
-DeviceModule g_dev[kMaxDevices];
-std::mutex g_mu;
+fmha_internal::ModuleCache<4> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
 
-void set_err(char* err, size_t errlen, const char* fmt, ...) {
-    if (!err || errlen == 0) return;
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(err, errlen, fmt, ap);
-    va_end(ap);
-}
-
-int fail(char* err, size_t errlen, int code, const char* prefix, const char* msg) {
-    set_err(err, errlen, "%s: %s", prefix, msg);
-    return code;
-}
-
-// Loads the embedded code object on the current device (once per device, thread-safe).
-int get_functions(hipFunction_t** out, char* err, size_t errlen) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) {
-        set_err(err, errlen, "hipGetDevice: %s", hipGetErrorString(e));
-        return FMHA_ERR_NO_DEVICE;
-    }
-    if (dev < 0 || dev >= kMaxDevices) {
-        set_err(err, errlen, "device %d out of range", dev);
-        return FMHA_ERR_NO_DEVICE;
-    }
-    DeviceModule& dm = g_dev[dev];
-    if (!dm.loaded.load(std::memory_order_acquire)) {
-        std::lock_guard<std::mutex> lk(g_mu);
-        if (!dm.loaded.load(std::memory_order_relaxed)) {
-            hipModule_t mod = nullptr;
-            e = hipModuleLoadData(&mod, fmha_mxfp8_hsaco_begin);
-            if (e != hipSuccess) {
-                set_err(err, errlen, "hipModuleLoadData (gfx950 code object, %zu bytes): %s",
-                        (size_t)(fmha_mxfp8_hsaco_end - fmha_mxfp8_hsaco_begin), hipGetErrorString(e));
-                return FMHA_ERR_NO_DEVICE;
-            }
-            for (int i = 0; i < 4; ++i) {
-                e = hipModuleGetFunction(&dm.fn[i], mod, kKernelNames[i]);
-                if (e != hipSuccess) {
-                    set_err(err, errlen, "hipModuleGetFunction(%s): %s", kKernelNames[i], hipGetErrorString(e));
-                    (void)hipModuleUnload(mod);
-                    return FMHA_ERR_NO_DEVICE;
-                }
-            }
-            dm.mod = mod;
-            dm.loaded.store(true, std::memory_order_release);
-        }
-    }
-    *out = dm.fn;
-    return FMHA_OK;
-}
+int get_functions(hipFunction_t** out, char* err, size_t errlen) { return g_fmha.get(out, err, errlen); }
 
 int launch_raw(int which, const void* args, size_t nbytes, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block,
                void* stream, char* err, size_t errlen) {
-    hipFunction_t* fns = nullptr;
-    int rc = get_functions(&fns, err, errlen);
-    if (rc != FMHA_OK) return rc;
-    size_t sz = nbytes;
-    void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(args), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
-                     HIP_LAUNCH_PARAM_END};
-    hipError_t e = hipModuleLaunchKernel(fns[which], gx, gy, gz, block, 1, 1, 0, (hipStream_t)stream, nullptr, extra);
-    if (e != hipSuccess) {
-        set_err(err, errlen, "hipModuleLaunchKernel(%s): %s", kKernelNames[which], hipGetErrorString(e));
-        return FMHA_ERR_HIP;
-    }
-    return FMHA_OK;
+    return g_fmha.launch(which, args, nbytes, gx, gy, gz, block, stream, err, errlen);
 }
 
 typedef long long i64;

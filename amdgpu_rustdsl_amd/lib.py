@@ -90,11 +90,18 @@ _L.fmha_fwd_hd128_mxfp8_auto.argtypes = [_P(Params), _vp, _sz, _vp, _P(_c), _P(_
 _L.fmha_mxfp8_init.argtypes = [_cp, _sz]
 _L.fmha_mxfp8_version.restype = _cp
 _L.fmha_mxfp8_version.argtypes = []
+# include/mxfp8_quant.h
+_L.fmha_mxfp8_quantize_rows.argtypes = [_vp, _vp, _vp, _i64, ctypes.c_float, _u64, _u64, _u64, _vp, _cp, _sz]
+_L.fmha_mxfp8_quantize_tensor.argtypes = [_vp, _vp, _vp, _i64, _u64, _u64, _u64, _vp, _cp, _sz]
+_L.fmha_mxfp8_quantize_seq32.argtypes = [_vp, _vp, _vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _u64, _u64, _u64, _vp, _cp, _sz]
+_L.fmha_mxfp8_seq32_scale_bytes.argtypes = [_i64, _i64, _i64]
+_L.fmha_mxfp8_seq32_scale_bytes.restype = _sz
 
 EXPORTED = ["fmha_mxfp8_validate_vs128", "fmha_mxfp8_validate_t128", "fmha_mxfp8_validate_kvsplit", "fmha_mxfp8_validate_combine",
             "fmha_mxfp8_select_path", "fmha_mxfp8_fill_args", "fmha_mxfp8_workspace_bytes", "fmha_mxfp8_launch_vs128",
             "fmha_mxfp8_launch_t128", "fmha_mxfp8_launch_kvsplit", "fmha_mxfp8_launch_combine", "fmha_fwd_hd128_mxfp8_auto",
-            "fmha_mxfp8_init", "fmha_mxfp8_version"]
+            "fmha_mxfp8_init", "fmha_mxfp8_version",
+            "fmha_mxfp8_quantize_rows", "fmha_mxfp8_quantize_tensor", "fmha_mxfp8_quantize_seq32", "fmha_mxfp8_seq32_scale_bytes"]
 
 raw = _L
 
@@ -161,3 +168,22 @@ def run_auto(params, workspace=None, workspace_bytes=0, stream=None):
                                       ctypes.byref(splits), buf, 512)
     check(rc, buf)
     return PATH_NAMES[path.value], splits.value
+
+
+def quantize_rows(x, q, scale, rows, mul, bytes_x, bytes_q, bytes_scale, stream=None):
+    buf = _errbuf()
+    check(_L.fmha_mxfp8_quantize_rows(x, q, scale, rows, mul, bytes_x, bytes_q, bytes_scale, stream, buf, 512), buf)
+
+
+def quantize_tensor(x, q, descale, n, bytes_x, bytes_q, bytes_descale, stream=None):
+    buf = _errbuf()
+    check(_L.fmha_mxfp8_quantize_tensor(x, q, descale, n, bytes_x, bytes_q, bytes_descale, stream, buf, 512), buf)
+
+
+def quantize_seq32(x, q, scale, B, SK, HK, bytes_x, bytes_q, bytes_scale, stream=None):
+    buf = _errbuf()
+    check(_L.fmha_mxfp8_quantize_seq32(x, q, scale, B, SK, HK, bytes_x, bytes_q, bytes_scale, stream, buf, 512), buf)
+
+
+def seq32_scale_bytes(B, SK, HK):
+    return int(_L.fmha_mxfp8_seq32_scale_bytes(B, SK, HK))

@@ -118,34 +118,94 @@ def alloc_scales(B, rows, H, device, fill=0):
     return view
 
 
-def quantize_mxfp8(x, scale_out, mul=1.0):
-    """Quantise fp32 rows x[..., 128] to MXFP8 as the reference's generator does (ref_host.cpp:239-251): per 32-element
-    block E8M0 = clamp(floor(log2 amax) - 8 + 127, 0, 254), elements e4m3 round-to-nearest-even saturating at 448.
-    Writes the scales into ``scale_out`` (same leading shape, last dim 4) and returns the e4m3 bytes (uint8)."""
-    xb = (x.float() * mul).reshape(*x.shape[:-1], 4, 32)
-    amax = xb.abs().amax(dim=-1)
-    e = torch.where(amax > 0, torch.floor(torch.log2(amax)) - 8, torch.full_like(amax, -127.0))
-    eb = torch.clamp(e + 127, 0, 254)
-    scale_out.copy_(eb.to(torch.uint8))
-    y = xb * torch.exp2(-(eb - 127)).unsqueeze(-1)
-    y = torch.clamp(y, -448.0, 448.0)
-    return y.to(torch.float8_e4m3fn).view(torch.uint8).reshape(x.shape)
+def _bf16(x, name, rows=True):
+    if not isinstance(x, torch.Tensor) or x.device.type != "cuda":
+        raise ValueError(f"{name}: expected a device tensor")
+    if rows and x.shape[-1] != D:
+        raise ValueError(f"{name}: expected a last dimension of {D}, got {tuple(x.shape)}")
+    return x.to(torch.bfloat16).contiguous()
+
+
+def _stream(dev, stream):
+    return stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
+
+
+def quantize_mxfp8(x, scale_out, mul=1.0, stream=None):
+    """On-GPU MXFP8 quantisation of rows x[..., 128] (bf16; other dtypes are cast to bf16 first) by the reference's
+    generator rule (ref_host.cpp:239-247): per 32-element block E8M0 = clamp(floor(log2 amax) - 8 + 127, 0, 254) of
+    the block of ``x * mul`` (f32), elements e4m3 round-to-nearest-even saturating at 448. Writes the scales into
+    ``scale_out`` (uint8, shape x.shape[:-1] + (4,); ``alloc_scales`` gives one with the FMHA's zeroed slack) and
+    returns the e4m3 bytes (uint8, shape of x). Runs fmha_mxfp8_quantize_rows (include/mxfp8_quant.h)."""
+    xb = _bf16(x, "x")
+    rows = xb.numel() // D
+    _expect(scale_out, "scale_out", tuple(x.shape[:-1]) + (4,), 1, align=4)
+    q = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        lib.quantize_rows(xb.data_ptr(), q.data_ptr(), scale_out.data_ptr(), rows, float(mul), _cap(xb), _cap(q), _cap(scale_out),
+                          _stream(x.device, stream))
+    return q
+
+
+def quantize_v(x, stream=None):
+    """On-GPU V quantisation with one f32 descale per tensor (ref_host.cpp:248-251): d = amax / 448, q = e4m3(x / d).
+    Returns (q uint8 of x's shape, v_scale: a 4096-byte f32 buffer with d in element 0, the FMHA's V descale
+    argument). x may have any shape whose element count is a multiple of 8. Runs fmha_mxfp8_quantize_tensor."""
+    xb = _bf16(x, "x", rows=False)
+    q = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    vs = torch.zeros(1024, dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        lib.quantize_tensor(xb.data_ptr(), q.data_ptr(), vs.data_ptr(), xb.numel(), _cap(xb), _cap(q), _cap(vs), _stream(x.device, stream))
+    return q, vs
+
+
+def quantize_v_seq32(x, stream=None):
+    """On-GPU V quantisation with one E8M0 per 32 keys along the sequence and per head_dim column (an extension; the
+    reference's V scale is one f32 per tensor). x [B, SK, HK, 128] -> (q uint8 [B, SK, HK, 128],
+    scale uint8 [B, ceil(SK/32), HK, 128]). Runs fmha_mxfp8_quantize_seq32."""
+    if x.dim() != 4:
+        raise ValueError(f"x: expected [B, SK, HK, 128], got {tuple(x.shape)}")
+    B, SK, HK, _ = x.shape
+    xb = _bf16(x, "x")
+    q = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    sc = torch.empty(B, (SK + 31) // 32, HK, D, dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        lib.quantize_seq32(xb.data_ptr(), q.data_ptr(), sc.data_ptr(), B, SK, HK, _cap(xb), _cap(q), _cap(sc), _stream(x.device, stream))
+    return q, sc
+
+
+LOG2E_OVER_SQRT_D = 1.4426950408889634 / math.sqrt(D)
+
+
+def fmha_fwd_bf16_via_mxfp8(q, k, v, out=None, *, softmax_scale=None, causal=False, path="auto", splits=None, lse=None, stream=None):
+    """Attention from bf16 q [B, S, H, 128], k / v [B, SK, HK, 128]: quantises on the GPU (Q scaled by
+    softmax_scale * log2(e) before quantisation, default 1/sqrt(128), as ref_host.cpp:238 folds it), then runs
+    ``fmha_fwd_mxfp8``. Returns out (bf16 [B, S, H, 128]); ``lse``, when given, receives the natural-log LSE of
+    the scaled scores."""
+    B, S, H, _ = q.shape
+    _, SK, HK, _ = k.shape
+    mul = LOG2E_OVER_SQRT_D if softmax_scale is None else 1.4426950408889634 * float(softmax_scale)
+    qs = alloc_scales(B, S, H, q.device)
+    ks = alloc_scales(B, SK, HK, k.device)
+    q8 = quantize_mxfp8(q, qs, mul=mul, stream=stream)
+    k8 = quantize_mxfp8(k, ks, stream=stream)
+    v8, vs = quantize_v(v, stream=stream)
+    if out is None:
+        out = torch.empty(B, S, H, D, dtype=torch.bfloat16, device=q.device)
+    fmha_fwd_mxfp8(q8, k8, v8, qs, ks, vs, out, path=path, splits=splits, stream=stream, lse=lse, causal=causal)
+    return out
 
 
 def random_inputs(B, H, S, SK, HK=None, device="cuda", seed=0):
     """Synthetic MXFP8 inputs with the distribution of the reference's REF_DATA=normal generator
-    (N(0,1) Q/K/V, Q x log2(e)/sqrt(128), per-32 E8M0 along head_dim, V e4m3 with one f32 descale),
-    drawn on the device with torch's generator. Returns (q, k, v, q_scale, k_scale, v_scale)."""
+    (N(0,1) Q/K/V, Q x log2(e)/sqrt(128), per-32 E8M0 along head_dim, V e4m3 with one f32 descale), drawn on the
+    device with torch's generator in bf16 and quantised by the on-GPU quantisers.
+    Returns (q, k, v, q_scale, k_scale, v_scale)."""
     HK = HK or H
     g = torch.Generator(device=device)
     g.manual_seed(seed)
     qs = alloc_scales(B, S, H, device)
     ks = alloc_scales(B, SK, HK, device)
-    q = quantize_mxfp8(torch.randn(B, S, H, D, generator=g, device=device), qs, mul=1.4426950408889634 / math.sqrt(D))
-    k = quantize_mxfp8(torch.randn(B, SK, HK, D, generator=g, device=device), ks)
-    vv = torch.randn(B, SK, HK, D, generator=g, device=device)
-    vd = (vv.abs().amax() / 448.0).float()
-    v = torch.clamp(vv / vd, -448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
-    vs = torch.zeros(1024, dtype=torch.float32, device=device)
-    vs[0] = vd
+    q = quantize_mxfp8(torch.randn(B, S, H, D, generator=g, device=device, dtype=torch.bfloat16), qs, mul=LOG2E_OVER_SQRT_D)
+    k = quantize_mxfp8(torch.randn(B, SK, HK, D, generator=g, device=device, dtype=torch.bfloat16), ks)
+    v, vs = quantize_v(torch.randn(B, SK, HK, D, generator=g, device=device, dtype=torch.bfloat16))
     return q, k, v, qs, ks, vs

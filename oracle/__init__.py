@@ -75,6 +75,12 @@ def lib():
         L.mxo_emulate.argtypes = [ctypes.POINTER(Problem), i, i, vp, vp, vp, i]
         L.mxo_combine.restype = None
         L.mxo_combine.argtypes = [vp, vp, vp, ctypes.c_long, i]
+        L.mxo_quant_rows_bf16.argtypes = [vp, ctypes.c_long, f, vp, vp]
+        L.mxo_quant_rows_bf16.restype = None
+        L.mxo_quant_tensor_bf16.argtypes = [vp, ctypes.c_long, vp]
+        L.mxo_quant_tensor_bf16.restype = f
+        L.mxo_quant_seq32_bf16.argtypes = [vp, i, i, i, vp, vp]
+        L.mxo_quant_seq32_bf16.restype = None
         _lib = L
     return _lib
 
@@ -164,3 +170,30 @@ def combine(ohat, lse, rows_total, splits):
 
 def bf16_to_f32(a):
     return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def quant_rows_bf16(x, mul=1.0):
+    """x: uint16 bf16 bits [rows*128] -> (e4m3 bytes [rows*128], E8M0 bytes [rows*4]) by the generator's rule."""
+    x = np.ascontiguousarray(x, np.uint16).reshape(-1)
+    rows = x.size // D
+    q = np.zeros(rows * D, np.uint8)
+    sc = np.zeros(rows * 4, np.uint8)
+    lib().mxo_quant_rows_bf16(_ptr(x), rows, mul, _ptr(q), _ptr(sc))
+    return q, sc
+
+
+def quant_tensor_bf16(x):
+    """x: uint16 bf16 bits [n] -> (e4m3 bytes [n], f32 descale)."""
+    x = np.ascontiguousarray(x, np.uint16).reshape(-1)
+    q = np.zeros(x.size, np.uint8)
+    d = lib().mxo_quant_tensor_bf16(_ptr(x), x.size, _ptr(q))
+    return q, np.float32(d)
+
+
+def quant_seq32_bf16(x, B, SK, HK):
+    """x: uint16 bf16 bits [B*SK*HK*128] -> (e4m3 bytes, E8M0 bytes [B*ceil(SK/32)*HK*128])."""
+    x = np.ascontiguousarray(x, np.uint16).reshape(-1)
+    q = np.zeros(x.size, np.uint8)
+    sc = np.zeros(B * ((SK + 31) // 32) * HK * D, np.uint8)
+    lib().mxo_quant_seq32_bf16(_ptr(x), B, SK, HK, _ptr(q), _ptr(sc))
+    return q, sc

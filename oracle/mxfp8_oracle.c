@@ -662,3 +662,63 @@ void mxo_combine(const uint16_t* ohat_f16, const float* lse, uint16_t* out_bf16,
         for (int d = 0; d < D; ++d) out_bf16[(size_t)r * D + d] = mxo_f32_to_bf16(acc[d] * rd);
     }
 }
+
+/* ---- quantisers of bf16 inputs (the generator's rule, ref_host.cpp:239-251, applied to given values) ---- */
+
+static int e8m0_rule(double amax) {
+    /* ref_host.cpp:243-244. +-Inf maxima are outside the generator's domain (its int cast of floor(log2(inf)) is
+     * undefined); the library defines them as exponent field 255 - 8 = 247, and so does this restatement. */
+    if (isinf(amax)) return 247;
+    const int e = amax > 0 ? (int)floor(log2(amax)) - 8 : -127;
+    int eb = e + 127;
+    if (eb < 0) eb = 0;
+    if (eb > 254) eb = 254;
+    return eb;
+}
+
+static double running_max(double amax, double a) { return amax < a ? a : amax; }   /* std::max(amax, a) */
+
+void mxo_quant_rows_bf16(const uint16_t* x, long rows, float mul, uint8_t* q, uint8_t* sc) {
+    for (long r = 0; r < rows; ++r)
+        for (int bk = 0; bk < 4; ++bk) {
+            float y[32];
+            double amax = 0;
+            for (int i = 0; i < 32; ++i) {
+                y[i] = mxo_bf16_to_f32(x[(size_t)r * D + 32 * bk + i]) * mul;
+                amax = running_max(amax, fabs((double)y[i]));
+            }
+            const int eb = e8m0_rule(amax);
+            sc[(size_t)r * 4 + bk] = (uint8_t)eb;
+            const double inv = ldexp(1.0, -(eb - 127));
+            for (int i = 0; i < 32; ++i) q[(size_t)r * D + 32 * bk + i] = mxo_e4m3_encode_sat((float)(y[i] * inv));
+        }
+}
+
+float mxo_quant_tensor_bf16(const uint16_t* x, long n, uint8_t* q) {
+    /* ref_host.cpp:248-251: vdescale = (float)(vmax / 448), v = e4m3((float)(x / vdescale)) */
+    double vmax = 0;
+    for (long i = 0; i < n; ++i) vmax = running_max(vmax, fabs((double)mxo_bf16_to_f32(x[i])));
+    const float d = (float)(vmax / 448.0);
+    for (long i = 0; i < n; ++i) q[i] = mxo_e4m3_encode_sat((float)((double)mxo_bf16_to_f32(x[i]) / d));
+    return d;
+}
+
+void mxo_quant_seq32_bf16(const uint16_t* x, int B, int SK, int HK, uint8_t* q, uint8_t* sc) {
+    const int nblk = (SK + 31) / 32;
+    for (int b = 0; b < B; ++b)
+        for (int blk = 0; blk < nblk; ++blk)
+            for (int h = 0; h < HK; ++h)
+                for (int d = 0; d < D; ++d) {
+                    const int k0 = 32 * blk, nk = SK - k0 < 32 ? SK - k0 : 32;
+                    double amax = 0;
+                    for (int k = 0; k < nk; ++k)
+                        amax = running_max(amax, fabs((double)mxo_bf16_to_f32(x[(((size_t)b * SK + k0 + k) * HK + h) * D + d])));
+                    const int eb = e8m0_rule(amax);
+                    sc[(((size_t)b * nblk + blk) * HK + h) * D + d] = (uint8_t)eb;
+                    const double inv = ldexp(1.0, -(eb - 127));
+                    for (int k = 0; k < nk; ++k) {
+                        const size_t i = (((size_t)b * SK + k0 + k) * HK + h) * D + d;
+                        q[i] = mxo_e4m3_encode_sat((float)(mxo_bf16_to_f32(x[i]) * inv));
+                    }
+                }
+}

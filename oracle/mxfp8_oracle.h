@@ -9,6 +9,9 @@
  * Contents and the reference code each part restates:
  *   mxo_e4m3_decode / mxo_e4m3_encode   tests/gpu/ref_host.cpp:26-33, 216-228
  *   mxo_generate                        tests/gpu/ref_host.cpp:183-263 (REF_DATA lcg | uniform | normal)
+ *   mxo_quant_rows_bf16 / _tensor_bf16 /
+ *   mxo_quant_seq32_bf16                the generator's quantisation rule (ref_host.cpp:239-251) applied to
+ *                                       given bf16 values (the checker of the on-GPU quantisers)
  *   mxo_select_path                     crates/amdgpu-graph/src/dispatch.rs:494-511
  *   mxo_split_range                     crates/amdgpu-stage/src/components.rs:58-74
  *   mxo_check_fp64                      tests/gpu/ref_host.cpp:436-471
@@ -72,6 +75,13 @@ float mxo_generate(int mode, int B, int H, int HK, int S, int SK, uint64_t seed_
                    uint8_t* q, uint8_t* k, uint8_t* v, uint8_t* qs, uint8_t* ks);
 
 /* Dispatch: returns 0 vs128, 1 t128, 2 kvsplit; *splits set for kvsplit. */
+/* x [rows,128] bf16 -> q [rows,128] e4m3 + sc [rows,4] E8M0; x is multiplied by `mul` in f32 first. */
+void mxo_quant_rows_bf16(const uint16_t* x, long rows, float mul, uint8_t* q, uint8_t* sc);
+/* x [n] bf16 -> q [n] e4m3; returns the f32 descale amax / 448. */
+float mxo_quant_tensor_bf16(const uint16_t* x, long n, uint8_t* q);
+/* x [B,SK,HK,128] bf16 -> q (same shape) e4m3 + sc [B,ceil(SK/32),HK,128] E8M0 (per 32 keys per column). */
+void mxo_quant_seq32_bf16(const uint16_t* x, int B, int SK, int HK, uint8_t* q, uint8_t* sc);
+
 int mxo_select_path(long B, long H, long S, long SK, int* splits);
 /* KV-split range of split `s`: [*key_lo, *key_lo + *kv_eff). */
 void mxo_split_range(int SK, int splits, int s, int* key_lo, int* kv_eff);

@@ -342,3 +342,88 @@ def test_emulated_partials_combine_to_emulated_output():
     out, ohat, lse = oracle.emulate(inp, splits=splits, rows=0, partials=True)
     merged = oracle.combine(ohat, lse, inp.B * inp.S * inp.H, splits)
     np.testing.assert_array_equal(merged, out)
+
+
+# ------------------------------------------------------------------ quantisers of bf16 inputs
+
+_E4M3 = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+
+
+def _f32_to_bf16_bits(a):
+    return (np.asarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_quant_rows_reproduces_the_generator():
+    """The generator's own output (q, E8M0) dequantised to bf16 (exact: 4 significant bits) and quantised again by
+    the restated rule gives back the generator's bytes. Its blocks' largest element lies in [256, 448], so the
+    rule must return the same exponent; the only change allowed is -0 (0x80, a negative value that rounded to
+    zero) coming back as +0, since the generator's sign byte is `x < 0` (ref_host.cpp:219)."""
+    inp = oracle.Inputs(2, 4, 96, 80, HK=2)
+    for x, s in ((inp.q, inp.qs), (inp.k, inp.ks)):
+        rows = x.size // D
+        sc = s[: rows * 4].reshape(rows, 4)
+        val = _E4M3[x.reshape(rows, 4, 32)] * np.exp2(sc.astype(np.float64) - 127)[:, :, None]
+        bits = _f32_to_bf16_bits(val.astype(np.float32))
+        assert np.array_equal(oracle.bf16_to_f32(bits).reshape(val.shape), val.astype(np.float32))
+        q2, s2 = oracle.quant_rows_bf16(bits)
+        assert np.array_equal(s2, sc.reshape(-1))
+        want = np.where(x == 0x80, 0, x)
+        assert np.array_equal(q2, want)
+
+
+def test_quant_rows_known_answers():
+    """Hand-evaluated ref_host.cpp:243-247 on single blocks. amax 500 = 1.95 2^8: E8M0 = 8 - 8 + 127 = 127 and 500
+    saturates to 448 (0x7E); the GEMM family's ceil(log2(amax / 448)) rule would give 128 and 250 -> 0x77 instead.
+    amax 256: 127, 256 -> 0x78. amax 2^-130 (a bf16 subnormal): clamps to E8M0 0, element 2^-130 2^127 = 2^-3 ->
+    0x20. An all-zero block: E8M0 0, bytes 0."""
+    x = np.zeros((1, D), np.float32)
+    x[0, 0], x[0, 1] = 500.0, -1.0
+    x[0, 32] = 256.0
+    x[0, 64] = 2.0 ** -130
+    q, s = oracle.quant_rows_bf16(_f32_to_bf16_bits(x))
+    assert list(s) == [127, 127, 0, 0]
+    assert q[0] == 0x7E and q[1] == 0xB8 and q[32] == 0x78 and q[64] == 0x20
+    assert (q[96:] == 0).all()
+    # the multiplier applies before the block maximum: 2 x 250 = 500 again
+    x2 = x.copy()
+    x2[0, 0] = 250.0
+    q2, s2 = oracle.quant_rows_bf16(_f32_to_bf16_bits(x2), 2.0)
+    assert s2[0] == 127 and q2[0] == 0x7E
+
+
+def test_quant_tensor_closed_form():
+    """ref_host.cpp:248-251 with amax 448 (descale exactly 1) and 896 (descale 2): e4m3 grid values come back as
+    their own bytes, midpoints between neighbours go to the even byte, magnitudes past 448 saturate."""
+    pos = _E4M3[:127].astype(np.float32)
+    mids = ((pos[:-1] + pos[1:]) / 2).astype(np.float32)
+    exact_mids = mids[_f32_to_bf16_bits(mids).astype(np.uint32) << 16 == mids.view(np.uint32)]
+    for scale in (1.0, 2.0):
+        x = np.concatenate([pos, -pos, exact_mids, [448.0]]).astype(np.float32) * scale
+        x = np.concatenate([x, np.zeros((-x.size) % 8, np.float32)])
+        q, d = oracle.quant_tensor_bf16(_f32_to_bf16_bits(x))
+        assert d == np.float32(scale)
+        n = pos.size
+        assert np.array_equal(q[:n], np.arange(127))
+        assert np.array_equal(q[n:2 * n], np.where(np.arange(127) == 0, 0, np.arange(127) | 0x80))
+        i = np.searchsorted(pos, exact_mids)
+        assert np.array_equal(q[2 * n:2 * n + exact_mids.size], np.where(i % 2 == 0, i, i - 1))
+    q, d = oracle.quant_tensor_bf16(_f32_to_bf16_bits(np.array([1000.0, -1.0, 0, 0, 0, 0, 0, 0], np.float32)))
+    assert d == np.float32(1000.0 / 448.0) and q[0] == 0x7E
+
+
+@pytest.mark.parametrize("B,SK,HK", [(1, 64, 1), (2, 45, 3)])
+def test_quant_seq32_is_rows_rule_on_transposed_blocks(B, SK, HK):
+    """Blocks along the sequence = the rows rule applied to the transposed [column, 32 keys] block (zero-padded
+    keys past a ragged end change no maximum)."""
+    rng = np.random.default_rng(SK)
+    x = (rng.standard_normal((B, SK, HK, D)) * np.exp(rng.uniform(-8, 8, (B, SK, HK, D)))).astype(np.float32)
+    bits = _f32_to_bf16_bits(x)
+    q, s = oracle.quant_seq32_bf16(bits, B, SK, HK)
+    nb = (SK + 31) // 32
+    pad = np.zeros((B, nb * 32, HK, D), np.uint16)
+    pad[:, :SK] = bits
+    t = pad.reshape(B, nb, 32, HK, D).transpose(0, 1, 3, 4, 2)          # [B, nb, HK, D, 32 keys]
+    qr, sr = oracle.quant_rows_bf16(t.reshape(-1, 128))                  # 4 columns of 32 keys per row of 128
+    assert np.array_equal(s, sr)
+    qt = qr.reshape(B, nb, HK, D, 32).transpose(0, 1, 4, 2, 3).reshape(B, nb * 32, HK, D)[:, :SK]
+    assert np.array_equal(q.reshape(B, SK, HK, D), qt)
