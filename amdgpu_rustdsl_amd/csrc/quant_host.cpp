@@ -1,7 +1,7 @@
 // quant_host.cpp - host side of the MXFP8 quantisers: the C ABI of include/mxfp8_quant.h.
 //
 // Argument checks, then launches of the kernels of quant_kernels.hip (embedded at build time, loaded once per
-// device). No call allocates device memory; the V tensor scale uses the caller's descale buffer for its amax word.
+// device). No call allocates device memory; the V tensor scale keeps its partial maxima in the caller's descale buffer.
 
 #include <hip/hip_runtime.h>
 
@@ -54,21 +54,24 @@ static_assert(sizeof(QuantRowsArgs) == 40, "rows kernarg");
 static_assert(sizeof(QuantTensorArgs) == 32, "tensor kernarg");
 static_assert(sizeof(QuantSeq32Args) == 40, "seq32 kernarg");
 
-const char* const kQuantNames[5] = {
-    "fmha_mxfp8_quant_rows", "fmha_mxfp8_quant_clear", "fmha_mxfp8_quant_amax", "fmha_mxfp8_quant_tensor",
-    "fmha_mxfp8_quant_seq32",
+const char* const kQuantNames[4] = {
+    "fmha_mxfp8_quant_rows", "fmha_mxfp8_quant_amax", "fmha_mxfp8_quant_tensor", "fmha_mxfp8_quant_seq32",
 };
-enum { Q_ROWS = 0, Q_CLEAR = 1, Q_AMAX = 2, Q_TENSOR = 3, Q_SEQ32 = 4 };
+enum { Q_ROWS = 0, Q_AMAX = 1, Q_TENSOR = 2, Q_SEQ32 = 3 };
+// quant_kernels.hip: the amax pass runs exactly 512 workgroups and leaves one partial maximum each in descale words
+// [512, 1024); the descale buffer therefore spans 4096 bytes, the size the FMHA requires of it anyway.
+constexpr uint32_t kAmaxGroups = 512;
+constexpr uint64_t kDescaleBytes = 4096;
 
-fmha_internal::ModuleCache<5> g_quant(mxfp8_quant_hsaco_begin, mxfp8_quant_hsaco_end, kQuantNames);
+fmha_internal::ModuleCache<4> g_quant(mxfp8_quant_hsaco_begin, mxfp8_quant_hsaco_end, kQuantNames);
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-// Workgroups of a grid-stride launch over `chunks` 8-element chunks: enough to cover the chunks once, at most
-// 16 per CU of a 256-CU part.
+// Workgroups of the quantising pass over `chunks` 8-element chunks: enough to cover the chunks once, at most 4 per CU
+// of a 256-CU part (each workgroup first reduces the 512 partial maxima, so fewer, longer workgroups read less).
 uint32_t stride_grid(uint64_t chunks) {
     const uint64_t g = (chunks + 255) / 256;
-    return (uint32_t)(g < 1 ? 1 : g > 4096 ? 4096 : g);
+    return (uint32_t)(g < 1 ? 1 : g > 1024 ? 1024 : g);
 }
 
 }  // namespace
@@ -77,7 +80,7 @@ extern "C" {
 
 int fmha_mxfp8_quantize_rows(const void* x, void* q, void* scale, int64_t rows, float mul, uint64_t bytes_x, uint64_t bytes_q,
                              uint64_t bytes_scale, void* stream, char* err, size_t errlen) {
-    if (rows < 1 || rows > (int64_t)0xFFFFFFFF * 16) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "rows outside [1, 2^36)");
+    if (rows < 1 || rows > (int64_t)0xFFFFFFFF * 64) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "rows outside [1, 2^38)");
     if (!x || !q || !scale) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "null pointer");
     if (!aligned(x, 16) || !aligned(q, 8) || !aligned(scale, 4))
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "x needs 16-byte, q 8-byte and scale 4-byte alignment");
@@ -86,7 +89,7 @@ int fmha_mxfp8_quantize_rows(const void* x, void* q, void* scale, int64_t rows, 
     if (bytes_q < r * 128) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "q: buffer smaller than rows * 128 bytes");
     if (bytes_scale < r * 4) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "scale: buffer smaller than rows * 4 bytes");
     QuantRowsArgs a = {x, q, scale, r, mul, 0u};
-    return g_quant.launch(Q_ROWS, &a, sizeof(a), (uint32_t)((r + 15) / 16), 1, 1, 256, stream, err, errlen);
+    return g_quant.launch(Q_ROWS, &a, sizeof(a), (uint32_t)((r + 63) / 64), 1, 1, 256, stream, err, errlen);   // 64 rows per workgroup
 }
 
 int fmha_mxfp8_quantize_tensor(const void* x, void* q, void* descale, int64_t n, uint64_t bytes_x, uint64_t bytes_q,
@@ -98,12 +101,10 @@ int fmha_mxfp8_quantize_tensor(const void* x, void* q, void* descale, int64_t n,
     const uint64_t un = (uint64_t)n;
     if (bytes_x < un * 2) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "x: buffer smaller than n * 2 bytes");
     if (bytes_q < un) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "q: buffer smaller than n bytes");
-    if (bytes_descale < 8) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "descale: buffer smaller than 8 bytes");
+    if (bytes_descale < kDescaleBytes) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "descale: buffer smaller than 4096 bytes");
     QuantTensorArgs a = {x, q, descale, un};
-    const uint32_t g = stride_grid(un / 8);
-    int rc = g_quant.launch(Q_CLEAR, &a, sizeof(a), 1, 1, 1, 64, stream, err, errlen);
-    if (rc == FMHA_OK) rc = g_quant.launch(Q_AMAX, &a, sizeof(a), g, 1, 1, 256, stream, err, errlen);
-    if (rc == FMHA_OK) rc = g_quant.launch(Q_TENSOR, &a, sizeof(a), g, 1, 1, 256, stream, err, errlen);
+    int rc = g_quant.launch(Q_AMAX, &a, sizeof(a), kAmaxGroups, 1, 1, 256, stream, err, errlen);
+    if (rc == FMHA_OK) rc = g_quant.launch(Q_TENSOR, &a, sizeof(a), stride_grid(un / 8), 1, 1, 256, stream, err, errlen);
     return rc;
 }
 

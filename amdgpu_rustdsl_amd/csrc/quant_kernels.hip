@@ -76,9 +76,12 @@ struct QuantRowsArgs {
 struct QuantTensorArgs {
     const uint16_t* x;   // [n] bf16, n % 8 == 0
     uint8_t* q;          // [n] e4m3
-    float* descale;      // [0]: the f32 descale written by quant_tensor; [1]: the amax bits (scratch)
+    float* descale;      // 1024 f32: [0] the descale; [kQuantPartial, +kQuantAmaxGroups) the amax pass's partials
     uint64_t n;
 };
+// The amax pass runs exactly this many workgroups (the host launches it so), one partial maximum each.
+constexpr uint32_t kQuantAmaxGroups = 512;
+constexpr uint32_t kQuantPartial = 512;
 
 struct QuantSeq32Args {
     const uint16_t* x;   // [B, SK, HK, 128] bf16
@@ -87,78 +90,135 @@ struct QuantSeq32Args {
     uint32_t B, SK, HK, nblk;
 };
 
-// Rows: 16 lanes per 128-element row (8 elements per lane), 4 lanes per 32-element block; 16 rows per 256-lane
-// workgroup. Lane 0 of a row writes the row's 4 scale bytes as one word.
+// Rows: 16 lanes per 128-element row (8 elements per lane), 4 lanes per 32-element block. A workgroup covers
+// kRowsPerGroup rows: each 16-lane group takes 4 rows 16 apart and issues their four 16-byte loads before using any
+// (64 bytes in flight per lane). Lane 0 of a row writes the row's 4 scale bytes as one word.
+constexpr uint32_t kRowsPerGroup = 64;
+
 extern "C" __global__ void __launch_bounds__(256) fmha_mxfp8_quant_rows(QuantRowsArgs a) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint64_t row = (uint64_t)blockIdx.x * 16u + (threadIdx.x >> 4);
     const uint32_t c = threadIdx.x & 15u;   // 8-element chunk of the row
-    const bool live = row < a.rows;
-    const uint64_t r = live ? row : 0;      // dead lanes (the last workgroup's tail) read row 0 and store nothing
-    const u32x4 w = *reinterpret_cast<const u32x4*>(a.x + r * 128u + c * 8u);
-    float v[8];
-    for (int i = 0; i < 4; ++i) {
-        v[2 * i] = bf16_lo(w[i]) * a.mul;
-        v[2 * i + 1] = bf16_hi(w[i]) * a.mul;
+    const uint64_t row0 = (uint64_t)blockIdx.x * kRowsPerGroup + (threadIdx.x >> 4);
+    u32x4 w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint64_t row = row0 + 16u * j;
+        const uint64_t r = row < a.rows ? row : 0;   // rows past the end (the last workgroup) read row 0, store nothing
+        w[j] = *reinterpret_cast<const u32x4*>(a.x + r * 128u + c * 8u);
     }
-    float m = 0.0f;
-    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));   // fmaxf drops NaN, as std::max(amax, NaN) keeps amax
-    m = quad_max(m);
-    const uint32_t e = e8m0_of_amax(m);
-    const float s = inv_scale(e);
-    u32x2 out;
-    out[0] = pack4_e4m3(sat448(scaled(v[0], s)), sat448(scaled(v[1], s)), sat448(scaled(v[2], s)), sat448(scaled(v[3], s)));
-    out[1] = pack4_e4m3(sat448(scaled(v[4], s)), sat448(scaled(v[5], s)), sat448(scaled(v[6], s)), sat448(scaled(v[7], s)));
-    // the row's four block bytes sit in lanes c = 0, 4, 8, 12 of its 16-lane group
     const uint32_t base = lane & ~15u;
-    const uint32_t e1 = __shfl(e, base + 4, 64), e2 = __shfl(e, base + 8, 64), e3 = __shfl(e, base + 12, 64);
-    if (!live) return;
-    *reinterpret_cast<u32x2*>(a.q + row * 128u + c * 8u) = out;
-    if (c == 0) *reinterpret_cast<uint32_t*>(a.scale + row * 4u) = e | (e1 << 8) | (e2 << 16) | (e3 << 24);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint64_t row = row0 + 16u * j;
+        float v[8];
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = bf16_lo(w[j][i]) * a.mul;
+            v[2 * i + 1] = bf16_hi(w[j][i]) * a.mul;
+        }
+        float m = 0.0f;
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));   // fmaxf drops NaN, as std::max(amax, NaN) keeps amax
+        m = quad_max(m);
+        const uint32_t e = e8m0_of_amax(m);
+        const float s = inv_scale(e);
+        u32x2 out;
+        out[0] = pack4_e4m3(sat448(scaled(v[0], s)), sat448(scaled(v[1], s)), sat448(scaled(v[2], s)), sat448(scaled(v[3], s)));
+        out[1] = pack4_e4m3(sat448(scaled(v[4], s)), sat448(scaled(v[5], s)), sat448(scaled(v[6], s)), sat448(scaled(v[7], s)));
+        // the row's four block bytes sit in lanes c = 0, 4, 8, 12 of its 16-lane group
+        const uint32_t e1 = __shfl(e, base + 4, 64), e2 = __shfl(e, base + 8, 64), e3 = __shfl(e, base + 12, 64);
+        if (row < a.rows) {
+            *reinterpret_cast<u32x2*>(a.q + row * 128u + c * 8u) = out;
+            if (c == 0) *reinterpret_cast<uint32_t*>(a.scale + row * 4u) = e | (e1 << 8) | (e2 << 16) | (e3 << 24);
+        }
+    }
 }
 
-// Tensor scale, step 1: clears the amax word (a kernel rather than a memset, so the sequence can be captured).
-extern "C" __global__ void fmha_mxfp8_quant_clear(QuantTensorArgs a) {
-    if (threadIdx.x == 0) reinterpret_cast<uint32_t*>(a.descale)[1] = 0u;
-}
-
-// Tensor scale, step 2: amax over the tensor. Non-negative f32 order as their bit patterns, so the per-workgroup
-// maxima combine with an unsigned atomic max. NaN elements are skipped (fmaxf), matching std::max in the
-// generator's running maximum.
+// Tensor scale, pass 1: kQuantAmaxGroups workgroups stride over the tensor; workgroup g stores its maximum |x| into
+// descale[kQuantPartial + g] (plain stores: every slot is rewritten by every call, so nothing needs clearing and no
+// two workgroups touch one address). NaN elements are skipped (fmaxf), as std::max skips them in the generator's
+// running maximum.
 extern "C" __global__ void __launch_bounds__(256) fmha_mxfp8_quant_amax(QuantTensorArgs a) {
     __shared__ float part[4];
     const uint64_t nchunk = a.n / 8u;
+    const uint64_t stride = (uint64_t)gridDim.x * 256u;
     float m = 0.0f;
-    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < nchunk; i += (uint64_t)gridDim.x * 256u) {
+    uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    for (; i + 3 * stride < nchunk; i += 4 * stride) {   // four 16-byte loads in flight per lane
+        u32x4 w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w[u] = *reinterpret_cast<const u32x4*>(a.x + (i + u * stride) * 8u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(bf16_lo(w[u][j])), fabsf(bf16_hi(w[u][j]))));
+    }
+    for (; i < nchunk; i += stride) {
         const u32x4 w = *reinterpret_cast<const u32x4*>(a.x + i * 8u);
         for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(bf16_lo(w[j])), fabsf(bf16_hi(w[j]))));
     }
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     if ((threadIdx.x & 63u) == 0) part[threadIdx.x >> 6] = m;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        m = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
-        atomicMax(reinterpret_cast<uint32_t*>(a.descale) + 1, __float_as_uint(m));
-    }
+    if (threadIdx.x == 0) a.descale[kQuantPartial + blockIdx.x] = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
 }
 
-// Tensor scale, step 3: d = amax / 448, q = e4m3(x / d), both divisions correctly rounded as the generator's
-// double divisions rounded to f32 are. Workgroup 0 writes d to descale[0].
+// Tensor scale, pass 2: every workgroup reduces the kQuantAmaxGroups partial maxima, then d = amax / 448 and
+// q = e4m3(x / d), both divisions correctly rounded as the generator's double divisions rounded to f32 are.
+// Workgroup 0 writes d to descale[0].
+//
+// x / d is computed as q1 = q0 + (x - q0 d) r with r = RN(1/d), q0 = RN(x r) and the remainder from one fused
+// multiply-add, which is the correctly rounded quotient (Markstein's theorem: r within half an ulp of 1/d, q0 within
+// one ulp of x/d, remainder exact) as long as nothing leaves the normal range. The lanes with d, x or q0 outside
+// [2^-96, 2^96] take the full division instead (zero x stays on the fast path: it yields +-0 either way). Checked
+// against the correctly rounded division for every bf16 x over 40000 divisors, all-ones and power-of-two
+// mantissas included.
+// The fast quotient of x / d, and whether it is valid (`ok` is cleared when x or the quotient is out of range).
+__device__ inline float div_fast(float x, float d, float r, bool& ok) {
+    const float q0 = x * r;
+    ok = ok && ((fabsf(x) >= 0x1p-96f && fabsf(q0) >= 0x1p-96f) || x == 0.0f);
+    return __builtin_fmaf(__builtin_fmaf(-q0, d, x), r, q0);
+}
+
 extern "C" __global__ void __launch_bounds__(256) fmha_mxfp8_quant_tensor(QuantTensorArgs a) {
-    const float amax = __uint_as_float(reinterpret_cast<const uint32_t*>(a.descale)[1]);
+    __shared__ float part[4];
+    float m = 0.0f;
+    for (uint32_t i = threadIdx.x; i < kQuantAmaxGroups; i += 256u) m = fmaxf(m, a.descale[kQuantPartial + i]);
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((threadIdx.x & 63u) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
     const float d = __fdiv_rn(amax, 448.0f);
+    const float r = __fdiv_rn(1.0f, d);
+    const bool dfast = d >= 0x1p-96f && d <= 0x1p96f;
     const uint64_t nchunk = a.n / 8u;
-    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < nchunk; i += (uint64_t)gridDim.x * 256u) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(a.x + i * 8u);
-        float y[8];
-        for (int j = 0; j < 4; ++j) {
-            y[2 * j] = sat448(__fdiv_rn(bf16_lo(w[j]), d) + 0.0f);   // +0: -0 -> +0 (see scaled)
-            y[2 * j + 1] = sat448(__fdiv_rn(bf16_hi(w[j]), d) + 0.0f);
+    const uint64_t stride = (uint64_t)gridDim.x * 256u;
+    // four chunks per pass, their loads issued together (chunks past the end read chunk 0 and store nothing)
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < nchunk; i += 4 * stride) {
+        u32x4 w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint64_t c = i + u * stride;
+            w[u] = *reinterpret_cast<const u32x4*>(a.x + (c < nchunk ? c : 0) * 8u);
         }
-        u32x2 out;
-        out[0] = pack4_e4m3(y[0], y[1], y[2], y[3]);
-        out[1] = pack4_e4m3(y[4], y[5], y[6], y[7]);
-        *reinterpret_cast<u32x2*>(a.q + i * 8u) = out;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            float y[8];
+            bool ok = dfast;
+            for (int j = 0; j < 4; ++j) {
+                y[2 * j] = div_fast(bf16_lo(w[u][j]), d, r, ok);
+                y[2 * j + 1] = div_fast(bf16_hi(w[u][j]), d, r, ok);
+            }
+            if (!ok) {   // rare: one out-of-range element sends its whole chunk through the full division
+                for (int j = 0; j < 4; ++j) {
+                    y[2 * j] = __fdiv_rn(bf16_lo(w[u][j]), d);
+                    y[2 * j + 1] = __fdiv_rn(bf16_hi(w[u][j]), d);
+                }
+            }
+            for (int j = 0; j < 8; ++j) y[j] = sat448(y[j] + 0.0f);   // +0: -0 -> +0 (see scaled)
+            u32x2 out;
+            out[0] = pack4_e4m3(y[0], y[1], y[2], y[3]);
+            out[1] = pack4_e4m3(y[4], y[5], y[6], y[7]);
+            const uint64_t c = i + u * stride;
+            if (c < nchunk) *reinterpret_cast<u32x2*>(a.q + c * 8u) = out;
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) a.descale[0] = d;
 }

@@ -31,6 +31,8 @@ WORKLOADS = {
     "cfg4": (2, 8, 8, 2048, 2048, True, "auto", None, "B2H8S2048 causal bottom-right (configs[3])"),
     "cfg5": (1, 8, 8, 128, 16384, False, "kvsplit", 8, "B1H8 Sq128 SK16384 split 8 (configs[4])"),
     "cfg1": (1, 1, 1, 256, 256, False, "auto", None, "B1H1S256 (configs[0], t128)"),
+    # the on-GPU quantisers producing cfg2's inputs from bf16 (not the headline metric; an HBM-bound side path)
+    "quant": (4, 8, 8, 2048, 2048, False, None, None, "MXFP8 quantisation of B4H8S2048 bf16 Q, K, V"),
 }
 
 
@@ -92,6 +94,8 @@ def main():
         return
     from amdgpu_rustdsl_amd import lib, ops
 
+    if args.workload == "quant":
+        return main_quant(args, torch, lib, ops)
     B, H, HK, S, SK, causal, path, splits, desc = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -169,6 +173,70 @@ def main():
         line["cpu_baseline"] = cpu_baseline(B, H, HK, S, SK, causal)
     else:
         line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+def main_quant(args, torch, lib, ops):
+    """One step = quantise the bf16 Q, K (rows, E8M0 per 32) and V (one f32 descale) of B4H8S2048 on the GPU.
+    value = algorithmic bytes (bf16 read once, e4m3 + scales written once) / step time, in GB/s; roofline = the rows
+    kernel on Q alone against HBM bandwidth."""
+    B, H, HK, S, SK, _, _, _, desc = WORKLOADS["quant"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    xq = torch.randn(B, S, H, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    xk = torch.randn(B, SK, HK, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    xv = torch.randn(B, SK, HK, 128, generator=g, device=dev, dtype=torch.bfloat16)
+    qs, ks = ops.alloc_scales(B, S, H, dev), ops.alloc_scales(B, SK, HK, dev)
+    q8, k8, v8 = (torch.empty(x.shape, dtype=torch.uint8, device=dev) for x in (xq, xk, xv))
+    vs = torch.zeros(1024, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    st = stream.cuda_stream
+    cap = ops._cap
+    mul = ops.LOG2E_OVER_SQRT_D
+    nq, nk = xq.numel(), xk.numel()
+
+    def rows_q():
+        lib.quantize_rows(xq.data_ptr(), q8.data_ptr(), qs.data_ptr(), nq // 128, mul, cap(xq), cap(q8), cap(qs), st)
+
+    def step():
+        rows_q()
+        lib.quantize_rows(xk.data_ptr(), k8.data_ptr(), ks.data_ptr(), nk // 128, 1.0, cap(xk), cap(k8), cap(ks), st)
+        lib.quantize_tensor(xv.data_ptr(), v8.data_ptr(), vs.data_ptr(), nk, cap(xv), cap(v8), cap(vs), st)
+
+    def timed(fn, n):
+        for _ in range(max(args.warmup // 10, 20)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return max(e0.elapsed_time(e1) / n, (time.perf_counter() - t0) * 1e3 / n)
+
+    steps = max(args.steps // 10, 10)
+    ms = timed(step, steps)
+    bytes_step = (nq * 3 + nq // 8) + (nk * 3 + nk // 8) + nk * 3 + 4
+    rows_ms = timed(rows_q, steps)
+    rows_bytes = nq * 3 + nq // 8
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    rows_gbs = rows_bytes / (rows_ms * 1e-3) / 1e9
+    print(f"bench quant: {steps} steps, {ms * 1e3:.2f} us/step; rows kernel {rows_ms * 1e3:.2f} us", file=sys.stderr)
+    line = {
+        "metric": "MXFP8 input quantisation GB/s (bf16 Q, K, V of B4H8S2048), 1 MI355X",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": max(args.warmup // 10, 20),
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 -> e4m3 + E8M0", "data": "synthetic N(0,1) bf16 drawn on the GPU",
+        "config": {"workload": desc, "B": B, "H": H, "HK": HK, "S": S, "SK": SK, "bytes_per_step": bytes_step},
+        "roofline": {"bound": "hbm", "achieved": round(rows_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(rows_gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": "fmha_mxfp8_quant_rows",
+                     "kernel_ms": round(rows_ms, 5)},
+        "cpu_baseline": None,
+    }
     print(json.dumps(line), flush=True)
 
 

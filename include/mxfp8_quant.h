@@ -37,7 +37,8 @@ int fmha_mxfp8_quantize_rows(const void* x, void* q, void* scale, int64_t rows, 
                              void* stream, char* err, size_t errlen);
 
 /* x [n] bf16 (n % 8 == 0, 16-byte aligned) -> q [n] e4m3, descale[0] = amax / 448 (f32).
- * descale[1] is used as the amax word between the three launches of the call (bytes_descale >= 8). */
+ * `descale` is the FMHA's V-descale buffer (bytes_descale >= 4096, as fmha_mxfp8.h requires of it): between the
+ * call's two launches, f32 words [512, 1024) hold per-workgroup partial maxima (rewritten by every call). */
 int fmha_mxfp8_quantize_tensor(const void* x, void* q, void* descale, int64_t n,
                                uint64_t bytes_x, uint64_t bytes_q, uint64_t bytes_descale,
                                void* stream, char* err, size_t errlen);

@@ -97,6 +97,27 @@ def test_tensor_every_pattern_finite(gpu):
     assert np.array_equal(_host(q), q_ref)
 
 
+def test_tensor_many_divisors(gpu):
+    """The quotient x / d (d = amax / 448) over many divisors: for each chosen maximum, every finite bf16 pattern at or
+    below it. Covers the fast quotient path and the full-division path (tiny and huge d, subnormal x and quotients)."""
+    pats = np.arange(65536, dtype=np.uint16)
+    f = oracle.bf16_to_f32(pats)
+    fin = pats[np.isfinite(f)]
+    amaxes = [2.0 ** e for e in (-133, -126, -100, -97, -96, -60, -8, 0, 9, 40, 96, 97, 127)]
+    amaxes += [np.float32(1.9921875) * 2.0 ** e for e in (-130, -96, -10, 0, 3, 95, 126)]   # all-ones bf16 mantissa
+    for am in amaxes:
+        a = np.float32(am)
+        keep = fin[np.abs(oracle.bf16_to_f32(fin)) <= a]
+        keep = np.concatenate([keep, _bf16_bits([a])])
+        keep = np.concatenate([keep, np.zeros((-keep.size) % 8, np.uint16)])
+        q, vs = ops.quantize_v(_dev(keep, gpu))
+        torch.cuda.synchronize()
+        q_ref, d_ref = oracle.quant_tensor_bf16(keep)
+        assert vs[0].item() == d_ref, f"amax {am}"
+        bad = np.flatnonzero(_host(q) != q_ref)
+        assert bad.size == 0, f"amax {am}: {bad.size} bytes differ"
+
+
 def test_tensor_all_zero(gpu):
     q, vs = ops.quantize_v(torch.zeros(64, D, dtype=torch.bfloat16, device=gpu))
     torch.cuda.synchronize()
@@ -106,7 +127,7 @@ def test_tensor_all_zero(gpu):
 
 
 def test_tensor_repeat_reuses_scale_buffer(gpu):
-    # the amax word is cleared on the GPU by every call: a second, smaller tensor gets its own descale
+    # every call rewrites the partial maxima it reads: a second, smaller tensor gets its own descale
     big = torch.randn(256, D, device=gpu, dtype=torch.bfloat16) * 10
     small = torch.randn(64, D, device=gpu, dtype=torch.bfloat16)
     q = torch.empty(256 * D, dtype=torch.uint8, device=gpu)
@@ -145,7 +166,7 @@ def test_rejections(gpu):
     with pytest.raises(lib.FmhaError, match="multiple of 8"):
         lib.quantize_tensor(x.data_ptr(), q.data_ptr(), s.data_ptr(), 12, 4096, 4096, 64, st)
     with pytest.raises(lib.FmhaError, match="GV-HOST-EXTENT"):
-        lib.quantize_tensor(x.data_ptr(), q.data_ptr(), s.data_ptr(), 16 * D, 4096, 4096, 4, st)
+        lib.quantize_tensor(x.data_ptr(), q.data_ptr(), s.data_ptr(), 16 * D, 4096, 4096, 4095, st)
 
 
 def test_fmha_from_bf16_uses_the_quantised_inputs(gpu):
