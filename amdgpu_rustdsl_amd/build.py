@@ -1,6 +1,6 @@
 """Build of the native library: the gfx950 code object and the C-ABI host library that embeds it.
 
-    python -m amdgpu_rustdsl_amd.build          # or __graft_entry__.build()
+    python amdgpu_rustdsl_amd/build.py         # or __graft_entry__.build()
 
 Outputs (in-tree, git-ignored, shipped with the source tree):
     amdgpu_rustdsl_amd/_build/fmha_mxfp8_gfx950.hsaco   the four FMHA kernels (hipcc --genco, gfx950 only)

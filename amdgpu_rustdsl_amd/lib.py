@@ -9,7 +9,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_build", "libfmha_mxfp8.so")
 
 if not os.path.exists(LIB_PATH):
-    raise ImportError(f"{LIB_PATH} is missing: build it with `python -m amdgpu_rustdsl_amd.build` "
+    raise ImportError(f"{LIB_PATH} is missing: build it with `python amdgpu_rustdsl_amd/build.py` "
                       "(or __graft_entry__.build()); the MXFP8 FMHA has no non-native fallback")
 
 _L = ctypes.CDLL(LIB_PATH)
