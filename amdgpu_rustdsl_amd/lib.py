@@ -12,6 +12,14 @@ if not os.path.exists(LIB_PATH):
     raise ImportError(f"{LIB_PATH} is missing: build it with `python amdgpu_rustdsl_amd/build.py` "
                       "(or __graft_entry__.build()); the MXFP8 FMHA has no non-native fallback")
 
+# A process must hold one HIP runtime. PyTorch-ROCm ships its own libamdhip64.so.7 (the same soname as ROCm's), so
+# torch, when importable, is imported first: the library then binds to the runtime torch already loaded. Loaded the
+# other way round, /opt/rocm's runtime and torch's both come up, and the one that starts second finds no device.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 _L = ctypes.CDLL(LIB_PATH)
 
 FMHA_OK, FMHA_ERR_EXTENT, FMHA_ERR_KA_RANGE, FMHA_ERR_KA_IS, FMHA_ERR_GRID, FMHA_ERR_SYM = 0, 1, 2, 3, 4, 5
