@@ -49,6 +49,33 @@ typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 namespace {
 
+#ifdef FMHA_IL_NOFENCE_A
+#define IL_FENCE_A() do { } while (0)
+#else
+#define IL_FENCE_A() __builtin_amdgcn_sched_barrier(0)
+#endif
+#ifdef FMHA_IL_NOFENCE_B
+#define IL_FENCE_B() do { } while (0)
+#else
+#define IL_FENCE_B() __builtin_amdgcn_sched_barrier(0)
+#endif
+// vs128 / kvsplit loop: QK-first MFMA phases and direct HBM -> LDS tile copies (the register-staged, PV-first loop
+// stays selectable for measurements with -DFMHA_STAGED_LOOP)
+#ifndef FMHA_STAGED_LOOP
+#ifndef FMHA_QF
+#define FMHA_QF 1
+#endif
+#ifndef FMHA_DMA
+#define FMHA_DMA 1
+#endif
+#endif
+
+#ifndef FMHA_IL_KDEPTH
+#define FMHA_IL_KDEPTH 1
+#endif
+#ifndef FMHA_IL_VDEPTH
+#define FMHA_IL_VDEPTH 1
+#endif
 #ifndef FMHA_PREFETCH
 #define FMHA_PREFETCH 2
 #endif
@@ -113,6 +140,13 @@ struct Prm {
 #define FMHA_LMARK(p, blk, t, k) do { } while (0)
 #define FMHA_LFLUSH(p, blk) do { } while (0)
 #define FMHA_LDECL do { } while (0)
+#endif
+
+#ifdef FMHA_TRACE_M
+// debug builds only: shader-clock stamps at fixed points of one tile's phases, lane 0 of each wave, vector stores
+#define FMHA_TM(w, i) do { if ((w).tm && ((threadIdx.x & 63u) == 0u)) (w).tm[i] = __builtin_amdgcn_s_memtime(); } while (0)
+#else
+#define FMHA_TM(w, i) do { } while (0)
 #endif
 
 #define KA_AS __attribute__((address_space(4)))
@@ -206,6 +240,18 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t by
 __device__ inline void lds_write16(uint32_t off, v4i v) { *(LDS_AS v4i*)(uintptr_t)off = v; }
 __device__ inline void lds_write4(uint32_t off, uint32_t v) { *(LDS_AS uint32_t*)(uintptr_t)off = v; }
 
+// One direct HBM -> LDS copy of 16 bytes per lane: lane L's bytes land at LDS address lds_base + 16 L. Written as inline
+// assembly so that the compiler does not see an LDS write: through the builtin it makes every later LDS read of the ring
+// wait for all outstanding copies (vmcnt(0)), which would expose their full latency once per phase. The ordering is
+// explicit instead: a copy is published by the barrier that follows the wait on its vmcnt (block_barrier_keep_dma).
+// M0 carries the LDS base; no compiler-generated code in these kernels uses M0.
+__device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory");
+}
+
 // Register-staged copy of one 128-key tile (K and V: 16 KiB each; K scales: 512 B) from HBM into an LDS ring
 // slot: load() issues the buffer loads into VGPRs, store() writes them (after the slot is free) with ds_write_b128.
 // Thread tid moves 16-byte chunk (tid & 7) of rows i NT/8 + tid/8, i < kN: each 8-thread group reads one
@@ -279,6 +325,39 @@ struct Stager {
         r.ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, ksoff, 0, 0);
     }
 
+    // Direct HBM -> LDS copies (buffer_load_dwordx4 ... lds), no VGPR round trip: copy i of wave w writes LDS rows
+    // [8 g, 8 g + 8) of the slot, g = i NT/64 + w, lane L the 16 bytes at (8 g + L / 8) 128 + 16 (L & 7), which hold logical
+    // chunk (L & 7) ^ swz(row) of that row. Row steps of NT/8 (a multiple of 16) leave swz unchanged, so the lane's
+    // source offset is the same for every copy (dmaoff) plus a scalar (i NT/8) rows. A lane past the resource's end
+    // gets zeros, exactly as the register-staged path.
+    uint32_t dmaoff;
+    __device__ __forceinline__ void init_dma() {
+        const uint32_t row = 8u * (tid >> 6) + ((tid & 63u) >> 3);
+        dmaoff = row * k_seq + (((tid & 7u) ^ swz(row)) << 4);
+    }
+    __device__ __forceinline__ void dma(uint32_t kkey0, bool kvalid, uint32_t kslot, uint32_t vkey0, bool vvalid, uint32_t vslot) const {
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb + (size_t)kkey0 * k_seq, tile_bytes(kkey0, kvalid, k_seq, kD));
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + (size_t)vkey0 * k_seq, tile_bytes(vkey0, vvalid, k_seq, kD));
+        const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const uint32_t kbase = slot_base(lds, kLdsK, kslot, kTileBytes), vbase = slot_base(lds, kLdsV, vslot, kTileBytes);
+#pragma unroll
+        for (int i = 0; i < kN; ++i) {
+            const uint32_t g = (uint32_t)i * (NT / 64) + w;
+            const uint32_t soff = __builtin_amdgcn_readfirstlane((uint32_t)i * (NT / 8) * k_seq);
+            dma16(rk, kbase + g * 1024u, dmaoff, soff);
+            dma16(rv, vbase + g * 1024u, dmaoff, soff);
+        }
+    }
+    // The K-scale words of tile [kkey0, kkey0 + 128) into ksr (register-staged: the upper k-group's copy is shifted)
+    __device__ __forceinline__ void load_ks(uint32_t kkey0, bool kvalid) {
+        const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksb + (size_t)kkey0 * ks_row, tile_bytes(kkey0, kvalid, ks_row, 4));
+        cur.ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, ksoff, 0, 0);
+    }
+    __device__ __forceinline__ void store_ks(uint32_t kslot) const {
+        const uint32_t ksw_base = tid < 256u ? slot_base(lds, kLdsKs, kslot, kKsSlot) : lds + kLdsKsDummy;
+        lds_write4(ksw_base + kswoff, cur.ksr >> ksshift);
+    }
+
     __device__ __forceinline__ void store_from(const Regs& r, uint32_t kslot, uint32_t vslot) const {
         const uint32_t kb_ = slot_base(lds, kLdsK, kslot, kTileBytes) + woff, vb_ = slot_base(lds, kLdsV, vslot, kTileBytes) + woff;
 #pragma unroll
@@ -302,6 +381,14 @@ __device__ inline void block_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts
 // The same barrier with the wave's last N LDS operations still in flight: LDS operations complete in order, so
 // lgkmcnt(N) drains everything issued before them (the wave's tile stores) and leaves N reads issued for the next
 // phase outstanding.
+// The barrier that publishes the direct HBM -> LDS copies issued one phase earlier: the wave's last M VMEM operations
+// (this phase's copies) stay in flight, everything older (vmcnt counts in issue order) has landed in LDS.
+template <int N, int M>
+__device__ inline void block_barrier_keep_dma() {
+    static_assert(N >= 0 && N <= 15 && M >= 0 && M <= 63, "waitcnt fields");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(%1)\n\ts_barrier" ::"n"(M), "n"(N) : "memory");
+}
+
 template <int N>
 __device__ inline void block_barrier_keep() {
     static_assert(N >= 0 && N <= 15, "lgkmcnt field");
@@ -424,6 +511,9 @@ struct Wave {
     v4f lacc;
     v4i qtmp[4];       // the lane's Q bytes between their load (init) and their LDS write (commit_q)
     uint32_t qsw;      // the lane's Q scale word, loaded by init
+#ifdef FMHA_TRACE_M
+    uint64_t* tm = nullptr;
+#endif
 
     // Q rows of this wave -> LDS (commit_q), swizzled like a K tile at kLdsQ + 4096 wave, after init() issued the loads
     __device__ __forceinline__ void commit_q() {
@@ -595,6 +685,78 @@ struct Wave {
         for (int i = 0; i < DEPTH; ++i) ring[i] = vfrag(vb, i >> 2, i & 3);
     }
 
+    // The MFMA phase with QK(t+1) first (i = 0..7: k-half c = i / 4, accumulator t4 = i % 4) and PV(t) second (i = 8..15:
+    // V^T fragment (j, dc) = ((i - 8) / 4, (i - 8) % 4), row sums at dc = 0), so that S(t+1) is complete while PV(t)
+    // runs: the row max of S(t+1) (a quarter behind each of the first PV MFMAs) moves out of the VALU phase into the
+    // MFMA shadow. It is the unmasked maximum: a tile that needs the causal/tail mask is masked, and its maximum
+    // taken again, in its VALU phase (a masked write of S here, under the MFMAs, made the register allocation spill). Operands are read DEPTH MFMAs ahead across the QK -> PV seam; the first
+    // DEPTH K fragments, the Q fragment of k-half 0 and the K-scale words come from qk_prefetch. Returns the row max.
+    struct QkPre {
+        v8i qf0;
+        uint32_t ksw[4];
+    };
+    __device__ __forceinline__ void qk_prefetch(uint32_t kslot, Ring& ring, QkPre& pre) const {
+        const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
+        const uint32_t ksb = slot_base(lds, kLdsKs, kslot, (uint32_t)kKsSlot);
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) ring[i] = frag(kb, i >> 2, 4096u * (uint32_t)(i & 3));
+        pre.qf0 = qfrag(0);
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) pre.ksw[t4] = kscale(ksb, t4);
+    }
+
+    template <bool QK>
+    __device__ __forceinline__ float m_phase_qf(uint32_t vslot, const uint32_t (&pw)[4][4], uint32_t kslot, v16f (&s)[4], Ring& ring,
+                                                const QkPre& pre) {
+        const uint32_t vb = slot_base(lds, kLdsV, vslot, kTileBytes);
+        const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
+        constexpr int I0 = QK ? 0 : 8;
+#ifdef FMHA_EXP_NO_LDS_QF
+        // timing experiment only (wrong results): operands read once per phase
+        const v8i fk0 = frag(kb, 0), fv0 = vfrag(vb, 0, 0);
+        auto fetch = [&](int i) -> v8i { return i < 8 ? fk0 : fv0; };
+#else
+        auto fetch = [&](int i) -> v8i {
+            return i < 8 ? frag(kb, i >> 2, 4096u * (uint32_t)(i & 3)) : vfrag(vb, (i - 8) >> 2, (i - 8) & 3);
+        };
+#endif
+        v8i qf1;
+        v8i ones;
+        float mx = -1.0e30f;
+        if (!QK) {
+#pragma unroll
+            for (int i = I0; i < I0 + DEPTH; ++i) ring[i % (DEPTH + 1)] = fetch(i);
+            ones = ones_op();
+        }
+#pragma unroll
+        for (int i = I0; i < 16; ++i) {
+            if (i + DEPTH < 16) ring[(i + DEPTH) % (DEPTH + 1)] = fetch(i + DEPTH);
+            if (QK && i == 2) qf1 = qfrag(1);
+            if (QK && i == 5) ones = ones_op();
+            __builtin_amdgcn_sched_barrier(0);
+            if (i < 8) {
+                const int c = i >> 2, t4 = i & 3;
+                s[t4] = qk_mfma(ring[i % (DEPTH + 1)], c == 0 ? pre.qf0 : qf1, c == 0 ? s[3] : s[t4], pre.ksw[t4], c);
+            } else {
+                const int j = (i - 8) >> 2, dc = (i - 8) & 3;
+                const v8i pf = pfrag(pw, j);
+                if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, pf, lacc, 0, 0, 0, 127, 0, 127);
+                o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ring[i % (DEPTH + 1)], pf, o[dc], 0, 0, 0, 127, 0, 127);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // row max of S(t+1): accumulator (i - 9) behind PV MFMAs 9..12 (accumulator a's last QK MFMA is i = 4 + a)
+            if (QK && i >= 9 && i <= 12) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[i - 9][e]);
+                asm volatile("" : "+v"(mx));   // pins this quarter here (the reduction would otherwise sink past the MFMAs)
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (!QK) return 0.0f;
+        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx), __builtin_bit_cast(uint32_t, mx), false, false);
+        return fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
+    }
+
     template <bool PV, bool QK, typename Mid>
     __device__ __forceinline__ void m_phase(uint32_t vslot, const uint32_t (&pw)[4][4], uint32_t kslot, v16f (&s)[4], Ring& ring,
                                             Mid&& mid) {
@@ -653,6 +815,7 @@ struct Wave {
                 s[t4] = qk_mfma(ring[i % (DEPTH + 1)], qf[c], c == 0 ? s[3] : s[t4], ksw[t4], c);
                 if (i == 8) mid();
             }
+            FMHA_TM(*this, 8 + i);
             __builtin_amdgcn_sched_barrier(0);
         }
         if (!QK) mid();
@@ -769,6 +932,72 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
         // and V t+2 (a full iteration ahead of their store). In the interval before barrier t the reads touch K slots
         // t, t+1 and V slots t-1, t, the writes K slot t+2 and V slot t+1 (mod 3): disjoint, and every read tile was
         // written before the previous barrier.
+#ifdef FMHA_DMA
+        // K/V tiles go HBM -> LDS by direct copies. V(t) issues K tile t+2 and V tile t+1 into the slots the register-
+        // staged path writes in V(t), with the K-scale words (register-staged, loaded one phase ahead); the barrier that
+        // ends V(t+1) (A) or M(t+1) (B) waits for them (vmcnt counts in issue order: this phase's copies stay in flight).
+        constexpr int kDmaOps = 2 * Stager<NT>::kN + 1;   // VMEM operations issued per VALU phase
+        st.init_dma();
+        st.dma(key_of(0), true, 0, key_of(0), true, 0);                 // K 0, V 0
+        st.dma(key_of(1), ntiles > 1, 1, key_of(1), false, 2);          // K 1
+        st.load_ks(key_of(0), true);
+        st.store_ks(0);
+        st.load_ks(key_of(1), ntiles > 1);
+        st.store_ks(1);
+        st.load_ks(key_of(2), ntiles > 2);
+        w.commit_q();
+        asm volatile("s_waitcnt vmcnt(1)" ::: "memory");   // everything but the K-scale load of tile 2
+        FMHA_MARK(p, tblk, 2);
+        block_barrier();
+        FMHA_MARK(p, tblk, 3);
+        w.qk_all(0, s);
+        float mrow = row_max(s);   // unmasked row max of the tile the next VALU phase decides on
+        {
+            typename Wave<NT>::Ring ring;
+            typename Wave<NT>::QkPre pre;
+            auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4], bool last) {
+                FMHA_SETPRIO(0);
+                st.store_ks(slot_of(t + 2));
+                st.dma(key_of(t + 2), t + 2 < ntiles, slot_of(t + 2), key_of(t + 1), t + 1 < ntiles, slot_of(t + 1));
+                st.load_ks(key_of(t + 3), t + 3 < ntiles);
+                if (w.needs_mask(key_of(t))) {
+                    w.apply_mask(s, key_of(t));
+                    mrow = row_max(s);
+                }
+                rebase<LUT>(rc, mrow, s, w.o, w.lacc, w.bias, w.bw);
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
+                if (!last) {
+                    s[3] = splat16(w.bias);
+                    w.qk_prefetch(slot_of(t + 1), ring, pre);
+                }
+                FMHA_LMARK(p, tblk, t, 0);
+                // A: the copies of the previous VALU phase have landed; this phase's and the prefetched reads stay in flight
+                if (!GB) block_barrier_keep_dma<2 * Wave<NT>::DEPTH, kDmaOps>();
+                if (GB) asm volatile("" ::: "memory");
+                FMHA_LMARK(p, tblk, t, 1);
+                FMHA_SETPRIO(1);
+            };
+            uint32_t t = 0;
+            for (; t + 1 < ntiles; ++t) {
+                uint32_t pw[4][4];
+                v_phase(t, pw, false);
+                mrow = w.template m_phase_qf<true>(slot_of(t), pw, slot_of(t + 1), s, ring, pre);
+                FMHA_LMARK(p, tblk, t, 2);
+                if (GB) block_barrier_keep_dma<0, kDmaOps>();
+                else asm volatile("" ::: "memory");   // A: the compiler-only fence where B has its barrier
+                FMHA_LMARK(p, tblk, t, 3);
+            }
+            {
+                // the last tile: PV only
+                uint32_t pw[4][4];
+                v_phase(t, pw, true);
+                (void)w.template m_phase_qf<false>(slot_of(t), pw, slot_of(t), s, ring, pre);
+                if (GB) block_barrier();
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no copy into LDS outlives the loop
+#else
         typename Stager<NT>::Regs r0, r1;
         st.load_into(r0, key_of(0), true, key_of(0), true);            // K 0, V 0
         st.load_into(r1, key_of(1), ntiles > 1, key_of(2), false);     // K 1 (its V part: zeros into V slot 2)
@@ -779,32 +1008,45 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
         FMHA_MARK(p, tblk, 2);
         block_barrier();
         FMHA_MARK(p, tblk, 3);
+#ifdef FMHA_QF
         w.qk_all(0, s);
         // Every wave runs every tile of the block's range: a tile that is fully masked for a wave's rows (causal
         // diagonal) gives P = 0 and no rebase, so the result is unchanged, and a single instantiation of the phase
         // code keeps the register allocation spill-free.
+        float mrow = row_max(s);   // unmasked row max of the tile the next VALU phase decides on
         {
             typename Wave<NT>::Ring ring;
-            auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4]) {
+            typename Wave<NT>::QkPre pre;
+            // V(t): staging, the rebase decision of tile t (its row max came with the previous MFMA phase), P(t), the
+            // seed of S(t+1) in s[3] and the first operands of M(t)
+            auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4], bool last) {
                 FMHA_SETPRIO(0);
+#ifdef FMHA_EXP_B_NOTHING
+                if (GB) { asm volatile("" ::: "memory"); return; }   // timing experiment only
+#endif
+#ifndef FMHA_EXP_NO_STAGE
                 st.store(slot_of(t + 2), slot_of(t + 1));   // zeros past the range: those slots are never read again
+#ifndef FMHA_EXP_NO_LOAD
                 // the next staging loads (K t+3, V t+2) right behind the stores: a full iteration of latency cover
                 st.load(key_of(t + 3), t + 3 < ntiles, key_of(t + 2), t + 2 < ntiles);
-#ifdef FMHA_EXP_NO_V
-                // timing experiment only (wrong results): no softmax work in the VALU phase
-#pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4)
-#pragma unroll
-                    for (int a = 0; a < 4; ++a) pw[t4][a] = __builtin_bit_cast(uint32_t, s[t4][a]);
 #else
-                if (w.needs_mask(key_of(t))) w.apply_mask(s, key_of(t));
-                rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
+                asm volatile("" : "+v"(st.cur.kr[0]), "+v"(st.cur.kr[1]), "+v"(st.cur.vr[0]), "+v"(st.cur.vr[1]), "+v"(st.cur.ksr));
+#endif
+#endif
+                if (w.needs_mask(key_of(t))) {
+                    w.apply_mask(s, key_of(t));
+                    mrow = row_max(s);
+                }
+                rebase<LUT>(rc, mrow, s, w.o, w.lacc, w.bias, w.bw);
 #pragma unroll
                 for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
-#endif
-                w.pv_prefetch(slot_of(t), ring);
+                if (!last) {
+                    s[3] = splat16(w.bias);
+                    w.qk_prefetch(slot_of(t + 1), ring, pre);
+                }
                 FMHA_LMARK(p, tblk, t, 0);
-                if (!GB) block_barrier_keep<4 * Wave<NT>::DEPTH>();   // A: the prefetched V^T reads stay in flight
+                // A: the prefetched operand reads stay in flight (at least the 2 DEPTH K-fragment reads follow the stores)
+                if (!GB) block_barrier_keep<2 * Wave<NT>::DEPTH>();
                 // B: a compiler-only memory fence where A has its barrier. Without one, the loop-invariant Q-fragment
                 // LDS reads get hoisted out of the loop and their registers stay live throughout (spills).
                 if (GB) asm volatile("" ::: "memory");
@@ -814,11 +1056,77 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
             uint32_t t = 0;
             for (; t + 1 < ntiles; ++t) {
                 uint32_t pw[4][4];
-                v_phase(t, pw);
-                w.template m_phase<true, true>(slot_of(t), pw, slot_of(t + 1), s, ring, [] {});
+                v_phase(t, pw, false);
+#if defined(FMHA_EXP_B_IDLE) || defined(FMHA_EXP_B_NOTHING)
+                if (!GB)   // timing experiment only (wrong results): group B skips its MFMA phases
+#endif
+                mrow = w.template m_phase_qf<true>(slot_of(t), pw, slot_of(t + 1), s, ring, pre);
                 FMHA_LMARK(p, tblk, t, 2);
                 if (GB) loop_barrier();
                 else asm volatile("" ::: "memory");   // A: the compiler-only fence where B has its barrier
+                FMHA_LMARK(p, tblk, t, 3);
+            }
+            {
+                // the last tile: PV only
+                uint32_t pw[4][4];
+                v_phase(t, pw, true);
+                (void)w.template m_phase_qf<false>(slot_of(t), pw, slot_of(t), s, ring, pre);
+                if (GB) block_barrier();
+            }
+        }
+#else
+        w.qk_all(0, s);
+        // Every wave runs every tile of the block's range: a tile that is fully masked for a wave's rows (causal
+        // diagonal) gives P = 0 and no rebase, so the result is unchanged, and a single instantiation of the phase
+        // code keeps the register allocation spill-free.
+        {
+            typename Wave<NT>::Ring ring;
+            auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4]) {
+                FMHA_SETPRIO(0);
+#ifdef FMHA_TRACE_M
+                w.tm = (t == 8u && p.trace) ? p.trace + 131072u + ((size_t)tblk * 8u + (threadIdx.x >> 6)) * 64u : nullptr;
+#endif
+                FMHA_TM(w, 0);
+                st.store(slot_of(t + 2), slot_of(t + 1));   // zeros past the range: those slots are never read again
+                FMHA_TM(w, 1);
+                // the next staging loads (K t+3, V t+2) right behind the stores: a full iteration of latency cover
+                st.load(key_of(t + 3), t + 3 < ntiles, key_of(t + 2), t + 2 < ntiles);
+                FMHA_TM(w, 2);
+#ifdef FMHA_EXP_NO_V
+                // timing experiment only (wrong results): no softmax work in the VALU phase
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+                    for (int a = 0; a < 4; ++a) pw[t4][a] = __builtin_bit_cast(uint32_t, s[t4][a]);
+#else
+                if (w.needs_mask(key_of(t))) w.apply_mask(s, key_of(t));
+                rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
+                FMHA_TM(w, 3);
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
+                FMHA_TM(w, 4);
+#endif
+                w.pv_prefetch(slot_of(t), ring);
+                FMHA_TM(w, 5);
+                FMHA_LMARK(p, tblk, t, 0);
+                if (!GB) block_barrier_keep<4 * Wave<NT>::DEPTH>();   // A: the prefetched V^T reads stay in flight
+                // B: a compiler-only memory fence where A has its barrier. Without one, the loop-invariant Q-fragment
+                // LDS reads get hoisted out of the loop and their registers stay live throughout (spills).
+                if (GB) asm volatile("" ::: "memory");
+                FMHA_TM(w, 6);
+                FMHA_LMARK(p, tblk, t, 1);
+                FMHA_SETPRIO(1);
+            };
+            uint32_t t = 0;
+            for (; t + 1 < ntiles; ++t) {
+                uint32_t pw[4][4];
+                v_phase(t, pw);
+                w.template m_phase<true, true>(slot_of(t), pw, slot_of(t + 1), s, ring, [] {});
+                FMHA_TM(w, 30);
+                FMHA_LMARK(p, tblk, t, 2);
+                if (GB) loop_barrier();
+                else asm volatile("" ::: "memory");   // A: the compiler-only fence where B has its barrier
+                FMHA_TM(w, 31);
                 FMHA_LMARK(p, tblk, t, 3);
             }
             {
@@ -829,6 +1137,8 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
                 if (GB) block_barrier();
             }
         }
+#endif
+#endif  // FMHA_DMA
         FMHA_SETPRIO(0);
     }
     FMHA_MARK(p, tblk, 4);
@@ -855,10 +1165,9 @@ __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint
 // computed and decided one iteration ahead. Iteration t: [P(t) conversion | QK(t+1)] then [PV(t) | row max of
 // S(t+1)]; the tile t+2 staged through registers lands in slot (t+2) % 3 (tile t-1's: its last read was in
 // iteration t-1), one barrier, then the rebase decision of tile t+1. The last tile runs [P | PV] alone.
-template <bool LUT>
+template <bool LUT, int NT = 256>
 __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_lo,
                                  uint32_t key_hi) {
-    constexpr int NT = 256;
     const Recipe rc = recipe(LUT);
     Wave<NT> w;
     w.init(p, lds, qtile, head, bidx, key_hi);
@@ -934,6 +1243,123 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
     epilogue<false>(p, w, head, bidx, 0, rc);
 }
 
+// Eight (or four) free-running waves, each overlapping its own VALU work with its own MFMAs (the pipelined order
+// above), with the VALU placed between the MFMAs explicitly: iteration t is
+//   A: for each 32-key accumulator a: convert S(t)[a] -> P(t)[a], then issue QK(t+1) k-half 0 into the same registers
+//      (the MFMA runs while the next accumulator converts); then k-half 1;
+//   B: PV(t) (8 MFMAs + 2 row-sum MFMAs), each followed by a quarter of the row max of S(t+1);
+//   C: the staged tile t+2 -> LDS slot (t+2) % 3, one barrier, the rebase decision of tile t+1.
+// A wave issues at most one VALU instruction every 8 cycles (16 for the fp8 conversions) while one 32x32x64 MFMA
+// keeps its SIMD's matrix pipe 64 cycles: interleaved, each wave's VALU runs under its own and its SIMD partner's
+// MFMAs instead of between them.
+template <bool LUT, bool SPLIT, int NT>
+__device__ void attend_interleaved(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split,
+                                   uint32_t key_lo, uint32_t key_hi) {
+    const Recipe rc = recipe(LUT);
+    Wave<NT> w;
+    w.init(p, lds, qtile, head, bidx, key_hi);
+    const uint32_t kvh = head / p.gqa;
+    const bool causal = (p.flags & 1u) != 0;
+    uint32_t key_end = key_hi;
+    if (causal) key_end = (uint32_t)max(0, min((int)key_hi, (int)(qtile * Wave<NT>::ROWS + Wave<NT>::ROWS - 1) + (int)p.SK - (int)p.S + 1));
+    const uint32_t ntiles = key_end > key_lo ? (key_end - key_lo + kTile - 1) / kTile : 0;
+    Stager<NT> st;
+    st.init(p.k + (size_t)bidx * p.k_b + kvh * kD, p.v + (size_t)bidx * p.v_b + kvh * kD, p.ks + (size_t)bidx * p.ks_b + kvh * 4u,
+            p.k_seq, p.SK, lds);
+    auto key_of = [&](uint32_t t) { return key_lo + t * kTile; };
+
+    v16f s[4];
+    if (ntiles > 0) {
+        typename Stager<NT>::Regs r0;
+        st.load_into(r0, key_of(0), true, key_of(0), true);
+        st.load(key_of(1), ntiles > 1, key_of(1), ntiles > 1);
+        w.commit_q();
+        st.store_from(r0, 0, 0);
+        if (ntiles > 1) st.store(1, 1);
+        block_barrier();
+        // Every wave runs every tile of the block's range (no per-wave branches in the loop, which would split the
+        // interleaved MFMA/VALU order): a tile fully masked for a wave's rows gives P = 0 and no rebase.
+        w.qk_all(0, s);
+        if (w.needs_mask(key_of(0))) w.apply_mask(s, key_of(0));
+        rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
+        uint32_t slot = 0;
+        for (uint32_t t = 0; t + 1 < ntiles; ++t) {
+            const uint32_t nslot = slot == 2u ? 0u : slot + 1u;
+            const uint32_t sslot = nslot == 2u ? 0u : nslot + 1u;   // slot of tile t+2
+            st.load(key_of(t + 2), t + 2 < ntiles, key_of(t + 2), t + 2 < ntiles);
+            uint32_t pw[4][4];
+            float m;
+            {
+                // A: P(t) conversion, accumulator by accumulator, under QK(t+1) k-half 0; then k-half 1
+                const uint32_t kb = slot_base(w.lds, kLdsK, nslot, kTileBytes), ksb = slot_base(w.lds, kLdsKs, nslot, (uint32_t)kKsSlot);
+                const v8i q0 = w.qfrag(0);
+                uint32_t ksw[4];
+#pragma unroll
+                for (int t4 = 0; t4 < 4; ++t4) ksw[t4] = w.kscale(ksb, t4);
+                constexpr int KD = FMHA_IL_KDEPTH;   // K fragments read this many MFMAs ahead
+                v8i kf[KD + 1];
+#pragma unroll
+                for (int g = 0; g < KD; ++g) kf[g] = w.frag(kb, g >> 2, 4096u * (uint32_t)(g & 3));
+                const v16f seed = splat16(w.bias);
+                v8i qf = q0;
+                IL_FENCE_A();
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    const int c = g >> 2, t4 = g & 3;
+                    if (g + KD < 8) kf[(g + KD) % (KD + 1)] = w.frag(kb, (g + KD) >> 2, 4096u * (uint32_t)((g + KD) & 3));
+                    if (g == 3) qf = w.qfrag(1);
+                    if (c == 0) convert_p<LUT>(rc, s[t4], pw[t4]);
+                    IL_FENCE_A();
+                    if (c == 0) s[t4] = w.qk_mfma(kf[g % (KD + 1)], g == 3 ? q0 : qf, seed, ksw[t4], 0);
+                    else s[t4] = w.qk_mfma(kf[g % (KD + 1)], qf, s[t4], ksw[t4], 1);
+                    IL_FENCE_A();
+                }
+            }
+            if (w.needs_mask(key_of(t + 1))) w.apply_mask(s, key_of(t + 1));
+            {
+                // B: PV(t), a quarter of the row max of S(t+1) behind each MFMA
+                const uint32_t vb = slot_base(w.lds, kLdsV, slot, kTileBytes);
+                constexpr int VD = FMHA_IL_VDEPTH;   // V fragments read this many MFMAs ahead
+                v8i vf[VD + 1];
+#pragma unroll
+                for (int g = 0; g < VD; ++g) vf[g] = w.vfrag(vb, g >> 2, g & 3);
+                const v8i ones = w.ones_op();
+                float mx = -1.0e30f;
+                IL_FENCE_B();
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    const int j = g >> 2, dc = g & 3;
+                    if (g + VD < 8) vf[(g + VD) % (VD + 1)] = w.vfrag(vb, (g + VD) >> 2, (g + VD) & 3);
+                    const v8i pf = Wave<NT>::pfrag(pw, j);
+                    if (dc == 0) w.lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, pf, w.lacc, 0, 0, 0, 127, 0, 127);
+                    w.o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[g % (VD + 1)], pf, w.o[dc], 0, 0, 0, 127, 0, 127);
+                    IL_FENCE_B();
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, s[g >> 1][8 * (g & 1) + i]);
+                    IL_FENCE_B();
+                }
+                m = mx;
+            }
+            {
+                const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m), false, false);
+                m = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
+            }
+            // C
+            if (t + 2 < ntiles) st.store(sslot, sslot);
+            block_barrier();
+            rebase<LUT>(rc, m, s, w.o, w.lacc, w.bias, w.bw);
+            slot = nslot;
+        }
+        {
+            uint32_t pw[4][4];
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
+            w.pv_all(slot, pw);
+        }
+    }
+    epilogue<SPLIT>(p, w, head, bidx, split, rc);
+}
+
 // Workgroup -> (q tile, head, z): consecutive tiles of one (batch, head) land on one XCD, so each XCD's L2 holds the K/V
 // its blocks share. The hardware deals workgroups round-robin over the 8 XCDs in linear order x + gx (y + gy z); when
 // n = gx gy is a multiple of 8 that XCD is (x + gx y) mod 8 in every z slice, and L -> (L mod 8) (n / 8) + L / 8
@@ -962,6 +1388,20 @@ __device__ void full_kernel(uint32_t lds) {
     uint32_t qt, head, z;
     block_coords(p.S, p.H, NT / 2, qt, head, z);
     const bool lut = (p.SK + 127u) / 128u < 4u;   // state.rs:75-77
+#ifdef FMHA_EXP_PIPE512
+    if (NT == 512) {
+        if (lut) attend_pipelined<true, 512>(p, lds, qt, head, z, 0, p.SK);
+        else attend_pipelined<false, 512>(p, lds, qt, head, z, 0, p.SK);
+        return;
+    }
+#endif
+#ifdef FMHA_EXP_IL512
+    if (NT == 512) {
+        if (lut) attend_interleaved<true, false, 512>(p, lds, qt, head, z, 0, 0, p.SK);
+        else attend_interleaved<false, false, 512>(p, lds, qt, head, z, 0, 0, p.SK);
+        return;
+    }
+#endif
     if (NT == 512) {
         if (lut) attend_pingpong<true, false>(p, lds, qt, head, z, 0, 0, p.SK);
         else attend_pingpong<false, false>(p, lds, qt, head, z, 0, 0, p.SK);
