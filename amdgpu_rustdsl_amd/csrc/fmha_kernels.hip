@@ -61,6 +61,9 @@ namespace {
 #endif
 // vs128 / kvsplit loop: QK-first MFMA phases and direct HBM -> LDS tile copies (the register-staged, PV-first loop
 // stays selectable for measurements with -DFMHA_STAGED_LOOP)
+#ifndef FMHA_Q_IN_LDS
+#define FMHA_QREG 1   // Q fragments stay in registers (16 VGPRs) instead of being re-read from LDS every tile
+#endif
 #ifndef FMHA_STAGED_LOOP
 #ifndef FMHA_QF
 #define FMHA_QF 1
@@ -386,7 +389,11 @@ __device__ inline void block_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts
 template <int N, int M>
 __device__ inline void block_barrier_keep_dma() {
     static_assert(N >= 0 && N <= 15 && M >= 0 && M <= 63, "waitcnt fields");
+#ifdef FMHA_EXP_NO_DMA_WAIT
+    asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");   // timing experiment only (races)
+#else
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(%1)\n\ts_barrier" ::"n"(M), "n"(N) : "memory");
+#endif
 }
 
 template <int N>
@@ -520,11 +527,13 @@ struct Wave {
         // Q scale bytes of the two k-halves (E8M0 - 9: S comes out x 2^-9)
 #pragma unroll
         for (int c = 0; c < 2; ++c) sq[c] = (int)(((qsw >> (8 * (2 * c + hh))) - 9u) & 0xffu);
+#ifndef FMHA_QREG
         const uint32_t qb = lds + kLdsQ + wave * 4096u;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
             for (int e = 0; e < 2; ++e) lds_write16(qb + (kfo ^ ((uint32_t)(4 * c + 2 * e) << 4)), qtmp[2 * c + e]);
+#endif
     }
 
     // Lane constants, softmax state, and the loads of the lane's Q bytes and scales. Q goes to LDS (commit_q) rather
@@ -596,7 +605,12 @@ struct Wave {
         return cat8(lds_read16(lane_addr(base, kfo ^ ((uint32_t)(4 * c) << 4)) + block_off),
                     lds_read16(lane_addr(base, kfo ^ ((uint32_t)(4 * c + 2) << 4)) + block_off));
     }
+#ifdef FMHA_QREG
+    // the lane's Q bytes stay in registers: fragment c = bytes [64 c + 16 hh, +16) and [64 c + 32 + 16 hh, +16) of its row
+    __device__ __forceinline__ v8i qfrag(int c) const { return cat8(qtmp[2 * c], qtmp[2 * c + 1]); }
+#else
     __device__ __forceinline__ v8i qfrag(int c) const { return frag(lds + kLdsQ + wave * 4096u, c); }
+#endif
     // K-scale word of 32-key block t4 for this lane's key row, read from the copy shifted down by hh bytes so that
     // op_sel byte 2c is the lane half's E8M0 byte 2c + hh
     __device__ __forceinline__ uint32_t kscale(uint32_t ksb, int t4) const { return lds_read4(lane_addr(ksb, kso) + 128u * t4); }
@@ -957,9 +971,15 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
             typename Wave<NT>::QkPre pre;
             auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4], bool last) {
                 FMHA_SETPRIO(0);
+#ifndef FMHA_EXP_NO_KS
                 st.store_ks(slot_of(t + 2));
+#endif
+#ifndef FMHA_EXP_NO_DMA
                 st.dma(key_of(t + 2), t + 2 < ntiles, slot_of(t + 2), key_of(t + 1), t + 1 < ntiles, slot_of(t + 1));
+#endif
+#ifndef FMHA_EXP_NO_KS
                 st.load_ks(key_of(t + 3), t + 3 < ntiles);
+#endif
                 if (w.needs_mask(key_of(t))) {
                     w.apply_mask(s, key_of(t));
                     mrow = row_max(s);
