@@ -18,9 +18,10 @@
 //   shorter: eager rebase when thr < m, thr = 120/512, target 131/512, LUT-corrected pknorm, P scale 1;
 //   P = e4m3(bf16_bits(pknorm_u16(S')) / scale) (a Schraudolph exp2: the u16 read as bf16 is 2^(512 S' - 127)).
 //
-// K/V/K-scale tiles are staged global -> LDS by global_load_lds_dwordx4 (no VGPR round trip) into a
-// double-buffered ring; 16-byte chunk c of LDS row r holds logical chunk c ^ swz(r), which makes both the
-// ds_read_b128 K reads and the transposing V reads bank-conflict free.
+// K/V tiles reach a 3-slot LDS ring by direct HBM -> LDS copies (buffer_load_dwordx4 ... lds) in vs128/kvsplit and
+// through registers in t128; 16-byte chunk c of LDS row r holds logical chunk c ^ swz(r), which makes both the
+// ds_read_b128 K reads and the transposing V reads bank-conflict free. The K-scale words go through registers (the
+// upper k-group reads a copy shifted by one byte). The Q fragments stay in registers.
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -39,46 +40,12 @@ typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 #define LDS_AS __attribute__((address_space(3)))
-// wave issue priority around the MFMA phases (measurement builds can turn it off)
-#ifdef FMHA_NO_SETPRIO
-#define FMHA_SETPRIO(x) do { } while (0)
-#else
+// wave issue priority around the MFMA phases
 #define FMHA_SETPRIO(x) __builtin_amdgcn_s_setprio(x)
-#endif
 #define GLOBAL_AS __attribute__((address_space(1)))
 
 namespace {
 
-#ifdef FMHA_IL_NOFENCE_A
-#define IL_FENCE_A() do { } while (0)
-#else
-#define IL_FENCE_A() __builtin_amdgcn_sched_barrier(0)
-#endif
-#ifdef FMHA_IL_NOFENCE_B
-#define IL_FENCE_B() do { } while (0)
-#else
-#define IL_FENCE_B() __builtin_amdgcn_sched_barrier(0)
-#endif
-// vs128 / kvsplit loop: QK-first MFMA phases and direct HBM -> LDS tile copies (the register-staged, PV-first loop
-// stays selectable for measurements with -DFMHA_STAGED_LOOP)
-#ifndef FMHA_Q_IN_LDS
-#define FMHA_QREG 1   // Q fragments stay in registers (16 VGPRs) instead of being re-read from LDS every tile
-#endif
-#ifndef FMHA_STAGED_LOOP
-#ifndef FMHA_QF
-#define FMHA_QF 1
-#endif
-#ifndef FMHA_DMA
-#define FMHA_DMA 1
-#endif
-#endif
-
-#ifndef FMHA_IL_KDEPTH
-#define FMHA_IL_KDEPTH 1
-#endif
-#ifndef FMHA_IL_VDEPTH
-#define FMHA_IL_VDEPTH 1
-#endif
 #ifndef FMHA_PREFETCH
 #define FMHA_PREFETCH 2
 #endif
@@ -89,8 +56,7 @@ constexpr int kTileBytes = kTile * kD;        // 16 KiB
 constexpr int kSlots = 3;                     // ring depth (prefetch distance 2)
 constexpr int kLdsK = 0;                      // kSlots K tiles
 constexpr int kLdsV = kSlots * kTileBytes;    // kSlots V tiles
-constexpr int kLdsQ = 2 * kSlots * kTileBytes;    // the block's Q rows (up to 256 x 128 B), swizzled like K
-constexpr int kLdsKs = kLdsQ + 256 * kD;          // kSlots x 1 KiB of K scales: the words, then the words >> 8
+constexpr int kLdsKs = 2 * kSlots * kTileBytes;   // kSlots x 1 KiB of K scales: the words, then the words >> 8
 constexpr int kKsSlot = 1024;
 constexpr int kLdsKsDummy = kLdsKs + kSlots * kKsSlot;   // 1 KiB sink for the K-scale writes of threads 256..511
 constexpr int kLdsBytes = kLdsKsDummy + 1024;
@@ -143,13 +109,6 @@ struct Prm {
 #define FMHA_LMARK(p, blk, t, k) do { } while (0)
 #define FMHA_LFLUSH(p, blk) do { } while (0)
 #define FMHA_LDECL do { } while (0)
-#endif
-
-#ifdef FMHA_TRACE_M
-// debug builds only: shader-clock stamps at fixed points of one tile's phases, lane 0 of each wave, vector stores
-#define FMHA_TM(w, i) do { if ((w).tm && ((threadIdx.x & 63u) == 0u)) (w).tm[i] = __builtin_amdgcn_s_memtime(); } while (0)
-#else
-#define FMHA_TM(w, i) do { } while (0)
 #endif
 
 #define KA_AS __attribute__((address_space(4)))
@@ -381,35 +340,14 @@ struct Stager {
 // later tile stay in flight across it.
 __device__ inline void block_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// The same barrier with the wave's last N LDS operations still in flight: LDS operations complete in order, so
-// lgkmcnt(N) drains everything issued before them (the wave's tile stores) and leaves N reads issued for the next
-// phase outstanding.
 // The barrier that publishes the direct HBM -> LDS copies issued one phase earlier: the wave's last M VMEM operations
-// (this phase's copies) stay in flight, everything older (vmcnt counts in issue order) has landed in LDS.
+// (this phase's copies) stay in flight, everything older (vmcnt counts in issue order) has landed in LDS; its LDS
+// operations are drained except the last N (the operand reads issued for the next phase).
 template <int N, int M>
 __device__ inline void block_barrier_keep_dma() {
     static_assert(N >= 0 && N <= 15 && M >= 0 && M <= 63, "waitcnt fields");
-#ifdef FMHA_EXP_NO_DMA_WAIT
-    asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");   // timing experiment only (races)
-#else
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(%1)\n\ts_barrier" ::"n"(M), "n"(N) : "memory");
-#endif
 }
-
-template <int N>
-__device__ inline void block_barrier_keep() {
-    static_assert(N >= 0 && N <= 15, "lgkmcnt field");
-#ifdef FMHA_EXP_NO_LOOP_BARRIER
-    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");   // timing experiment only (races)
-#else
-    asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
-#endif
-}
-#ifdef FMHA_EXP_NO_LOOP_BARRIER
-__device__ inline void loop_barrier() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-#else
-__device__ inline void loop_barrier() { block_barrier(); }
-#endif
 
 // Softmax recipe constants (softmax.rs:24-27 exact copy; softmax.rs:80-88 lazy copy).
 struct Recipe {
@@ -516,29 +454,18 @@ struct Wave {
     float bias;        // b of this lane's query: the seed of every S accumulator
     v16f o[4];
     v4f lacc;
-    v4i qtmp[4];       // the lane's Q bytes between their load (init) and their LDS write (commit_q)
+    v4i qtmp[4];       // the lane's Q bytes (32 B of the k-half c = 0 and 32 B of c = 1), resident for the whole range
     uint32_t qsw;      // the lane's Q scale word, loaded by init
-#ifdef FMHA_TRACE_M
-    uint64_t* tm = nullptr;
-#endif
 
-    // Q rows of this wave -> LDS (commit_q), swizzled like a K tile at kLdsQ + 4096 wave, after init() issued the loads
+    // Q scale operands from the scale word init() loaded (called once the load is likely back)
     __device__ __forceinline__ void commit_q() {
         // Q scale bytes of the two k-halves (E8M0 - 9: S comes out x 2^-9)
 #pragma unroll
         for (int c = 0; c < 2; ++c) sq[c] = (int)(((qsw >> (8 * (2 * c + hh))) - 9u) & 0xffu);
-#ifndef FMHA_QREG
-        const uint32_t qb = lds + kLdsQ + wave * 4096u;
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int e = 0; e < 2; ++e) lds_write16(qb + (kfo ^ ((uint32_t)(4 * c + 2 * e) << 4)), qtmp[2 * c + e]);
-#endif
     }
 
-    // Lane constants, softmax state, and the loads of the lane's Q bytes and scales. Q goes to LDS (commit_q) rather
-    // than staying in registers: the QK MFMAs read their B operand from there one k-half at a time, so only 8 Q VGPRs
-    // are live at the phase's register peak.
+    // Lane constants, softmax state, and the loads of the lane's Q bytes and scales. The Q bytes stay in registers
+    // (16 VGPRs) for the whole key range: re-reading them from LDS every tile cost 32 KiB of LDS reads per tile and block.
     __device__ __forceinline__ void init(const Prm& p, uint32_t lds_, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_hi_) {
         lane = threadIdx.x & 63u;
         wave = wave_id();
@@ -605,12 +532,8 @@ struct Wave {
         return cat8(lds_read16(lane_addr(base, kfo ^ ((uint32_t)(4 * c) << 4)) + block_off),
                     lds_read16(lane_addr(base, kfo ^ ((uint32_t)(4 * c + 2) << 4)) + block_off));
     }
-#ifdef FMHA_QREG
     // the lane's Q bytes stay in registers: fragment c = bytes [64 c + 16 hh, +16) and [64 c + 32 + 16 hh, +16) of its row
     __device__ __forceinline__ v8i qfrag(int c) const { return cat8(qtmp[2 * c], qtmp[2 * c + 1]); }
-#else
-    __device__ __forceinline__ v8i qfrag(int c) const { return frag(lds + kLdsQ + wave * 4096u, c); }
-#endif
     // K-scale word of 32-key block t4 for this lane's key row, read from the copy shifted down by hh bytes so that
     // op_sel byte 2c is the lane half's E8M0 byte 2c + hh
     __device__ __forceinline__ uint32_t kscale(uint32_t ksb, int t4) const { return lds_read4(lane_addr(ksb, kso) + 128u * t4); }
@@ -681,23 +604,8 @@ struct Wave {
         }
     }
 
-    // The MFMA phase of the two-group cadence as one software pipeline of 16 LDS-fed MFMAs: PV(t) (i = 0..7, V^T
-    // fragment (j, dc) = (i / 4, i % 4), plus the row sums at dc = 0) then QK(t+1) (i = 8..15, k-half c = (i - 8) / 4,
-    // accumulator t4 = (i - 8) % 4). The A operand of MFMA i is read from LDS two MFMAs ahead (a 3-deep register
-    // ring) across the PV -> QK seam, so an LDS round trip (longer than one 64-cycle MFMA under load) never stalls the
-    // matrix pipe; the Q fragments and K-scale words are read ahead the same way. `mid` runs after the first QK MFMA
-    // (the staging loads of a later tile: P and the V fragments are dead by then). A scheduling fence after every
-    // MFMA keeps the order.
     static constexpr int DEPTH = FMHA_PREFETCH;   // MFMA-phase operand reads run DEPTH MFMAs ahead
     typedef v8i Ring[DEPTH + 1];
-
-    // The first DEPTH V^T fragments of PV on slot `vslot`, read at the end of the VALU phase (the tile has been in LDS
-    // since before the phase began) so that the MFMA phase starts with an MFMA instead of an LDS round trip.
-    __device__ __forceinline__ void pv_prefetch(uint32_t vslot, Ring& ring) const {
-        const uint32_t vb = slot_base(lds, kLdsV, vslot, kTileBytes);
-#pragma unroll
-        for (int i = 0; i < DEPTH; ++i) ring[i] = vfrag(vb, i >> 2, i & 3);
-    }
 
     // The MFMA phase with QK(t+1) first (i = 0..7: k-half c = i / 4, accumulator t4 = i % 4) and PV(t) second (i = 8..15:
     // V^T fragment (j, dc) = ((i - 8) / 4, (i - 8) % 4), row sums at dc = 0), so that S(t+1) is complete while PV(t)
@@ -725,15 +633,9 @@ struct Wave {
         const uint32_t vb = slot_base(lds, kLdsV, vslot, kTileBytes);
         const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
         constexpr int I0 = QK ? 0 : 8;
-#ifdef FMHA_EXP_NO_LDS_QF
-        // timing experiment only (wrong results): operands read once per phase
-        const v8i fk0 = frag(kb, 0), fv0 = vfrag(vb, 0, 0);
-        auto fetch = [&](int i) -> v8i { return i < 8 ? fk0 : fv0; };
-#else
         auto fetch = [&](int i) -> v8i {
             return i < 8 ? frag(kb, i >> 2, 4096u * (uint32_t)(i & 3)) : vfrag(vb, (i - 8) >> 2, (i - 8) & 3);
         };
-#endif
         v8i qf1;
         v8i ones;
         float mx = -1.0e30f;
@@ -771,69 +673,6 @@ struct Wave {
         return fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
     }
 
-    template <bool PV, bool QK, typename Mid>
-    __device__ __forceinline__ void m_phase(uint32_t vslot, const uint32_t (&pw)[4][4], uint32_t kslot, v16f (&s)[4], Ring& ring,
-                                            Mid&& mid) {
-        const uint32_t vb = slot_base(lds, kLdsV, vslot, kTileBytes);
-        const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
-        const uint32_t ksb = slot_base(lds, kLdsKs, kslot, (uint32_t)kKsSlot);
-        constexpr int I0 = PV ? 0 : 8, I1 = QK ? 16 : 8;
-#ifdef FMHA_EXP_NO_LDS
-        // timing experiment only (wrong results): fragments read once per phase
-        const v8i fk = frag(kb, 0), fv = vfrag(vb, 0, 0);
-        auto fetch = [&](int i) -> v8i { return i < 8 ? fv : fk; };
-#else
-        auto fetch = [&](int i) -> v8i {
-            return i < 8 ? vfrag(vb, i >> 2, i & 3) : frag(kb, (i - 8) >> 2, 4096u * (uint32_t)((i - 8) & 3));
-        };
-#endif
-        v8i qf[2];
-        uint32_t ksw[4];
-        v8i ones;
-        if (PV) ones = ones_op();   // once per tile for both row-sum MFMAs
-        if (!PV) {   // with PV the caller prefetched the first fragments (pv_prefetch)
-#pragma unroll
-            for (int i = I0; i < I0 + DEPTH; ++i)
-                if (i < I1) ring[i % (DEPTH + 1)] = fetch(i);
-        }
-        if (!PV && QK) {
-            qf[0] = qfrag(0);
-#pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) ksw[t4] = kscale(ksb, t4);
-        }
-#pragma unroll
-        for (int i = I0; i < I1; ++i) {
-            if (i + DEPTH < I1) ring[(i + DEPTH) % (DEPTH + 1)] = fetch(i + DEPTH);
-            if (QK && i == (PV ? 6 : I0)) s[3] = splat16(bias);   // the seed of S (16 copies of b), before the first QK MFMA
-            if (PV && QK && i == 8 - DEPTH - 1) {
-                qf[0] = qfrag(0);
-#pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) ksw[t4] = kscale(ksb, t4);
-            }
-            if (QK && i == 10) qf[1] = qfrag(1);
-            // the reads above are issued before MFMA i (the scheduler would otherwise sink them past it)
-            __builtin_amdgcn_sched_barrier(0);
-#ifdef FMHA_EXP_NO_PV
-            if (i < 8) { (void)pw; } else
-#endif
-#ifdef FMHA_EXP_NO_QK
-            if (i >= 8) { (void)qf; if (i == 8) mid(); } else
-#endif
-            if (i < 8) {
-                const int j = i >> 2, dc = i & 3;
-                const v8i pf = pfrag(pw, j);
-                if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, pf, lacc, 0, 0, 0, 127, 0, 127);
-                o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ring[i % (DEPTH + 1)], pf, o[dc], 0, 0, 0, 127, 0, 127);
-            } else {
-                const int c = (i - 8) >> 2, t4 = (i - 8) & 3;
-                s[t4] = qk_mfma(ring[i % (DEPTH + 1)], qf[c], c == 0 ? s[3] : s[t4], ksw[t4], c);
-                if (i == 8) mid();
-            }
-            FMHA_TM(*this, 8 + i);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (!QK) mid();
-    }
 };
 
 // The row sum of this lane's query (the ones pattern puts it in D dword (lane / 16) % 2).
@@ -946,7 +785,6 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
         // and V t+2 (a full iteration ahead of their store). In the interval before barrier t the reads touch K slots
         // t, t+1 and V slots t-1, t, the writes K slot t+2 and V slot t+1 (mod 3): disjoint, and every read tile was
         // written before the previous barrier.
-#ifdef FMHA_DMA
         // K/V tiles go HBM -> LDS by direct copies. V(t) issues K tile t+2 and V tile t+1 into the slots the register-
         // staged path writes in V(t), with the K-scale words (register-staged, loaded one phase ahead); the barrier that
         // ends V(t+1) (A) or M(t+1) (B) waits for them (vmcnt counts in issue order: this phase's copies stay in flight).
@@ -971,15 +809,9 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
             typename Wave<NT>::QkPre pre;
             auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4], bool last) {
                 FMHA_SETPRIO(0);
-#ifndef FMHA_EXP_NO_KS
                 st.store_ks(slot_of(t + 2));
-#endif
-#ifndef FMHA_EXP_NO_DMA
                 st.dma(key_of(t + 2), t + 2 < ntiles, slot_of(t + 2), key_of(t + 1), t + 1 < ntiles, slot_of(t + 1));
-#endif
-#ifndef FMHA_EXP_NO_KS
                 st.load_ks(key_of(t + 3), t + 3 < ntiles);
-#endif
                 if (w.needs_mask(key_of(t))) {
                     w.apply_mask(s, key_of(t));
                     mrow = row_max(s);
@@ -1017,148 +849,6 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
             }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no copy into LDS outlives the loop
-#else
-        typename Stager<NT>::Regs r0, r1;
-        st.load_into(r0, key_of(0), true, key_of(0), true);            // K 0, V 0
-        st.load_into(r1, key_of(1), ntiles > 1, key_of(2), false);     // K 1 (its V part: zeros into V slot 2)
-        st.load(key_of(2), ntiles > 2, key_of(1), ntiles > 1);         // K 2, V 1: stored in V(0)
-        w.commit_q();
-        st.store_from(r0, 0, 0);
-        st.store_from(r1, 1, 2);
-        FMHA_MARK(p, tblk, 2);
-        block_barrier();
-        FMHA_MARK(p, tblk, 3);
-#ifdef FMHA_QF
-        w.qk_all(0, s);
-        // Every wave runs every tile of the block's range: a tile that is fully masked for a wave's rows (causal
-        // diagonal) gives P = 0 and no rebase, so the result is unchanged, and a single instantiation of the phase
-        // code keeps the register allocation spill-free.
-        float mrow = row_max(s);   // unmasked row max of the tile the next VALU phase decides on
-        {
-            typename Wave<NT>::Ring ring;
-            typename Wave<NT>::QkPre pre;
-            // V(t): staging, the rebase decision of tile t (its row max came with the previous MFMA phase), P(t), the
-            // seed of S(t+1) in s[3] and the first operands of M(t)
-            auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4], bool last) {
-                FMHA_SETPRIO(0);
-#ifdef FMHA_EXP_B_NOTHING
-                if (GB) { asm volatile("" ::: "memory"); return; }   // timing experiment only
-#endif
-#ifndef FMHA_EXP_NO_STAGE
-                st.store(slot_of(t + 2), slot_of(t + 1));   // zeros past the range: those slots are never read again
-#ifndef FMHA_EXP_NO_LOAD
-                // the next staging loads (K t+3, V t+2) right behind the stores: a full iteration of latency cover
-                st.load(key_of(t + 3), t + 3 < ntiles, key_of(t + 2), t + 2 < ntiles);
-#else
-                asm volatile("" : "+v"(st.cur.kr[0]), "+v"(st.cur.kr[1]), "+v"(st.cur.vr[0]), "+v"(st.cur.vr[1]), "+v"(st.cur.ksr));
-#endif
-#endif
-                if (w.needs_mask(key_of(t))) {
-                    w.apply_mask(s, key_of(t));
-                    mrow = row_max(s);
-                }
-                rebase<LUT>(rc, mrow, s, w.o, w.lacc, w.bias, w.bw);
-#pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
-                if (!last) {
-                    s[3] = splat16(w.bias);
-                    w.qk_prefetch(slot_of(t + 1), ring, pre);
-                }
-                FMHA_LMARK(p, tblk, t, 0);
-                // A: the prefetched operand reads stay in flight (at least the 2 DEPTH K-fragment reads follow the stores)
-                if (!GB) block_barrier_keep<2 * Wave<NT>::DEPTH>();
-                // B: a compiler-only memory fence where A has its barrier. Without one, the loop-invariant Q-fragment
-                // LDS reads get hoisted out of the loop and their registers stay live throughout (spills).
-                if (GB) asm volatile("" ::: "memory");
-                FMHA_LMARK(p, tblk, t, 1);
-                FMHA_SETPRIO(1);
-            };
-            uint32_t t = 0;
-            for (; t + 1 < ntiles; ++t) {
-                uint32_t pw[4][4];
-                v_phase(t, pw, false);
-#if defined(FMHA_EXP_B_IDLE) || defined(FMHA_EXP_B_NOTHING)
-                if (!GB)   // timing experiment only (wrong results): group B skips its MFMA phases
-#endif
-                mrow = w.template m_phase_qf<true>(slot_of(t), pw, slot_of(t + 1), s, ring, pre);
-                FMHA_LMARK(p, tblk, t, 2);
-                if (GB) loop_barrier();
-                else asm volatile("" ::: "memory");   // A: the compiler-only fence where B has its barrier
-                FMHA_LMARK(p, tblk, t, 3);
-            }
-            {
-                // the last tile: PV only
-                uint32_t pw[4][4];
-                v_phase(t, pw, true);
-                (void)w.template m_phase_qf<false>(slot_of(t), pw, slot_of(t), s, ring, pre);
-                if (GB) block_barrier();
-            }
-        }
-#else
-        w.qk_all(0, s);
-        // Every wave runs every tile of the block's range: a tile that is fully masked for a wave's rows (causal
-        // diagonal) gives P = 0 and no rebase, so the result is unchanged, and a single instantiation of the phase
-        // code keeps the register allocation spill-free.
-        {
-            typename Wave<NT>::Ring ring;
-            auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4]) {
-                FMHA_SETPRIO(0);
-#ifdef FMHA_TRACE_M
-                w.tm = (t == 8u && p.trace) ? p.trace + 131072u + ((size_t)tblk * 8u + (threadIdx.x >> 6)) * 64u : nullptr;
-#endif
-                FMHA_TM(w, 0);
-                st.store(slot_of(t + 2), slot_of(t + 1));   // zeros past the range: those slots are never read again
-                FMHA_TM(w, 1);
-                // the next staging loads (K t+3, V t+2) right behind the stores: a full iteration of latency cover
-                st.load(key_of(t + 3), t + 3 < ntiles, key_of(t + 2), t + 2 < ntiles);
-                FMHA_TM(w, 2);
-#ifdef FMHA_EXP_NO_V
-                // timing experiment only (wrong results): no softmax work in the VALU phase
-#pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4)
-#pragma unroll
-                    for (int a = 0; a < 4; ++a) pw[t4][a] = __builtin_bit_cast(uint32_t, s[t4][a]);
-#else
-                if (w.needs_mask(key_of(t))) w.apply_mask(s, key_of(t));
-                rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
-                FMHA_TM(w, 3);
-#pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
-                FMHA_TM(w, 4);
-#endif
-                w.pv_prefetch(slot_of(t), ring);
-                FMHA_TM(w, 5);
-                FMHA_LMARK(p, tblk, t, 0);
-                if (!GB) block_barrier_keep<4 * Wave<NT>::DEPTH>();   // A: the prefetched V^T reads stay in flight
-                // B: a compiler-only memory fence where A has its barrier. Without one, the loop-invariant Q-fragment
-                // LDS reads get hoisted out of the loop and their registers stay live throughout (spills).
-                if (GB) asm volatile("" ::: "memory");
-                FMHA_TM(w, 6);
-                FMHA_LMARK(p, tblk, t, 1);
-                FMHA_SETPRIO(1);
-            };
-            uint32_t t = 0;
-            for (; t + 1 < ntiles; ++t) {
-                uint32_t pw[4][4];
-                v_phase(t, pw);
-                w.template m_phase<true, true>(slot_of(t), pw, slot_of(t + 1), s, ring, [] {});
-                FMHA_TM(w, 30);
-                FMHA_LMARK(p, tblk, t, 2);
-                if (GB) loop_barrier();
-                else asm volatile("" ::: "memory");   // A: the compiler-only fence where B has its barrier
-                FMHA_TM(w, 31);
-                FMHA_LMARK(p, tblk, t, 3);
-            }
-            {
-                // the last tile: PV only
-                uint32_t pw[4][4];
-                v_phase(t, pw);
-                w.template m_phase<true, false>(slot_of(t), pw, slot_of(t), s, ring, [] {});
-                if (GB) block_barrier();
-            }
-        }
-#endif
-#endif  // FMHA_DMA
         FMHA_SETPRIO(0);
     }
     FMHA_MARK(p, tblk, 4);
@@ -1172,13 +862,8 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
 template <bool LUT, bool SPLIT>
 __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split,
                                 uint32_t key_lo, uint32_t key_hi) {
-#ifndef FMHA_LOCKSTEP
     if (wave_id() >= 4u) attend_pingpong_group<LUT, SPLIT, true>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
     else attend_pingpong_group<LUT, SPLIT, false>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
-#else
-    // measurement variant: all eight waves in lockstep (V | barrier | M); the slot schedule is race-free either way
-    attend_pingpong_group<LUT, SPLIT, false>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
-#endif
 }
 
 // One 4-wave group (_t128: one wave per SIMD, so each wave overlaps its own VALU with its own MFMAs): S(t) is
@@ -1263,123 +948,6 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
     epilogue<false>(p, w, head, bidx, 0, rc);
 }
 
-// Eight (or four) free-running waves, each overlapping its own VALU work with its own MFMAs (the pipelined order
-// above), with the VALU placed between the MFMAs explicitly: iteration t is
-//   A: for each 32-key accumulator a: convert S(t)[a] -> P(t)[a], then issue QK(t+1) k-half 0 into the same registers
-//      (the MFMA runs while the next accumulator converts); then k-half 1;
-//   B: PV(t) (8 MFMAs + 2 row-sum MFMAs), each followed by a quarter of the row max of S(t+1);
-//   C: the staged tile t+2 -> LDS slot (t+2) % 3, one barrier, the rebase decision of tile t+1.
-// A wave issues at most one VALU instruction every 8 cycles (16 for the fp8 conversions) while one 32x32x64 MFMA
-// keeps its SIMD's matrix pipe 64 cycles: interleaved, each wave's VALU runs under its own and its SIMD partner's
-// MFMAs instead of between them.
-template <bool LUT, bool SPLIT, int NT>
-__device__ void attend_interleaved(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split,
-                                   uint32_t key_lo, uint32_t key_hi) {
-    const Recipe rc = recipe(LUT);
-    Wave<NT> w;
-    w.init(p, lds, qtile, head, bidx, key_hi);
-    const uint32_t kvh = head / p.gqa;
-    const bool causal = (p.flags & 1u) != 0;
-    uint32_t key_end = key_hi;
-    if (causal) key_end = (uint32_t)max(0, min((int)key_hi, (int)(qtile * Wave<NT>::ROWS + Wave<NT>::ROWS - 1) + (int)p.SK - (int)p.S + 1));
-    const uint32_t ntiles = key_end > key_lo ? (key_end - key_lo + kTile - 1) / kTile : 0;
-    Stager<NT> st;
-    st.init(p.k + (size_t)bidx * p.k_b + kvh * kD, p.v + (size_t)bidx * p.v_b + kvh * kD, p.ks + (size_t)bidx * p.ks_b + kvh * 4u,
-            p.k_seq, p.SK, lds);
-    auto key_of = [&](uint32_t t) { return key_lo + t * kTile; };
-
-    v16f s[4];
-    if (ntiles > 0) {
-        typename Stager<NT>::Regs r0;
-        st.load_into(r0, key_of(0), true, key_of(0), true);
-        st.load(key_of(1), ntiles > 1, key_of(1), ntiles > 1);
-        w.commit_q();
-        st.store_from(r0, 0, 0);
-        if (ntiles > 1) st.store(1, 1);
-        block_barrier();
-        // Every wave runs every tile of the block's range (no per-wave branches in the loop, which would split the
-        // interleaved MFMA/VALU order): a tile fully masked for a wave's rows gives P = 0 and no rebase.
-        w.qk_all(0, s);
-        if (w.needs_mask(key_of(0))) w.apply_mask(s, key_of(0));
-        rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
-        uint32_t slot = 0;
-        for (uint32_t t = 0; t + 1 < ntiles; ++t) {
-            const uint32_t nslot = slot == 2u ? 0u : slot + 1u;
-            const uint32_t sslot = nslot == 2u ? 0u : nslot + 1u;   // slot of tile t+2
-            st.load(key_of(t + 2), t + 2 < ntiles, key_of(t + 2), t + 2 < ntiles);
-            uint32_t pw[4][4];
-            float m;
-            {
-                // A: P(t) conversion, accumulator by accumulator, under QK(t+1) k-half 0; then k-half 1
-                const uint32_t kb = slot_base(w.lds, kLdsK, nslot, kTileBytes), ksb = slot_base(w.lds, kLdsKs, nslot, (uint32_t)kKsSlot);
-                const v8i q0 = w.qfrag(0);
-                uint32_t ksw[4];
-#pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) ksw[t4] = w.kscale(ksb, t4);
-                constexpr int KD = FMHA_IL_KDEPTH;   // K fragments read this many MFMAs ahead
-                v8i kf[KD + 1];
-#pragma unroll
-                for (int g = 0; g < KD; ++g) kf[g] = w.frag(kb, g >> 2, 4096u * (uint32_t)(g & 3));
-                const v16f seed = splat16(w.bias);
-                v8i qf = q0;
-                IL_FENCE_A();
-#pragma unroll
-                for (int g = 0; g < 8; ++g) {
-                    const int c = g >> 2, t4 = g & 3;
-                    if (g + KD < 8) kf[(g + KD) % (KD + 1)] = w.frag(kb, (g + KD) >> 2, 4096u * (uint32_t)((g + KD) & 3));
-                    if (g == 3) qf = w.qfrag(1);
-                    if (c == 0) convert_p<LUT>(rc, s[t4], pw[t4]);
-                    IL_FENCE_A();
-                    if (c == 0) s[t4] = w.qk_mfma(kf[g % (KD + 1)], g == 3 ? q0 : qf, seed, ksw[t4], 0);
-                    else s[t4] = w.qk_mfma(kf[g % (KD + 1)], qf, s[t4], ksw[t4], 1);
-                    IL_FENCE_A();
-                }
-            }
-            if (w.needs_mask(key_of(t + 1))) w.apply_mask(s, key_of(t + 1));
-            {
-                // B: PV(t), a quarter of the row max of S(t+1) behind each MFMA
-                const uint32_t vb = slot_base(w.lds, kLdsV, slot, kTileBytes);
-                constexpr int VD = FMHA_IL_VDEPTH;   // V fragments read this many MFMAs ahead
-                v8i vf[VD + 1];
-#pragma unroll
-                for (int g = 0; g < VD; ++g) vf[g] = w.vfrag(vb, g >> 2, g & 3);
-                const v8i ones = w.ones_op();
-                float mx = -1.0e30f;
-                IL_FENCE_B();
-#pragma unroll
-                for (int g = 0; g < 8; ++g) {
-                    const int j = g >> 2, dc = g & 3;
-                    if (g + VD < 8) vf[(g + VD) % (VD + 1)] = w.vfrag(vb, (g + VD) >> 2, (g + VD) & 3);
-                    const v8i pf = Wave<NT>::pfrag(pw, j);
-                    if (dc == 0) w.lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, pf, w.lacc, 0, 0, 0, 127, 0, 127);
-                    w.o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[g % (VD + 1)], pf, w.o[dc], 0, 0, 0, 127, 0, 127);
-                    IL_FENCE_B();
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, s[g >> 1][8 * (g & 1) + i]);
-                    IL_FENCE_B();
-                }
-                m = mx;
-            }
-            {
-                const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m), false, false);
-                m = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
-            }
-            // C
-            if (t + 2 < ntiles) st.store(sslot, sslot);
-            block_barrier();
-            rebase<LUT>(rc, m, s, w.o, w.lacc, w.bias, w.bw);
-            slot = nslot;
-        }
-        {
-            uint32_t pw[4][4];
-#pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
-            w.pv_all(slot, pw);
-        }
-    }
-    epilogue<SPLIT>(p, w, head, bidx, split, rc);
-}
-
 // Workgroup -> (q tile, head, z): consecutive tiles of one (batch, head) land on one XCD, so each XCD's L2 holds the K/V
 // its blocks share. The hardware deals workgroups round-robin over the 8 XCDs in linear order x + gx (y + gy z); when
 // n = gx gy is a multiple of 8 that XCD is (x + gx y) mod 8 in every z slice, and L -> (L mod 8) (n / 8) + L / 8
@@ -1408,20 +976,6 @@ __device__ void full_kernel(uint32_t lds) {
     uint32_t qt, head, z;
     block_coords(p.S, p.H, NT / 2, qt, head, z);
     const bool lut = (p.SK + 127u) / 128u < 4u;   // state.rs:75-77
-#ifdef FMHA_EXP_PIPE512
-    if (NT == 512) {
-        if (lut) attend_pipelined<true, 512>(p, lds, qt, head, z, 0, p.SK);
-        else attend_pipelined<false, 512>(p, lds, qt, head, z, 0, p.SK);
-        return;
-    }
-#endif
-#ifdef FMHA_EXP_IL512
-    if (NT == 512) {
-        if (lut) attend_interleaved<true, false, 512>(p, lds, qt, head, z, 0, 0, p.SK);
-        else attend_interleaved<false, false, 512>(p, lds, qt, head, z, 0, 0, p.SK);
-        return;
-    }
-#endif
     if (NT == 512) {
         if (lut) attend_pingpong<true, false>(p, lds, qt, head, z, 0, 0, p.SK);
         else attend_pingpong<false, false>(p, lds, qt, head, z, 0, 0, p.SK);
