@@ -190,13 +190,16 @@ int fmha_mxfp8_validate_kvsplit(const fmha_mxfp8_kvsplit_args* ka, const fmha_mx
     fmha_mxfp8_args a;
     std::memcpy(&a, ka, 0x270);
     std::memset(reinterpret_cast<uint8_t*>(&a) + 0x270, 0, sizeof(a) - 0x270);
-    const i64 splits = ka->kvs_splits, rows = ka->kvs_rows_total;
+    // the split count is the low 16 bits; bit 16 is the f32-partials extension (FMHA_KVS_F32_PARTIALS)
+    const i64 splits = ka->kvs_splits & 0xffffu, rows = ka->kvs_rows_total;
+    const i64 row_bytes = 512;   // the workspace rows are fp32-sized in both formats
     int rc;
     if ((rc = rules_extent(a, *sz, B, err, errlen)) != FMHA_OK) return rc;
-    if (sz->ptr_ohat < (uint64_t)(splits * rows * 512)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_ohat: buffer ptr_ohat smaller than declared allocation");
+    if (sz->ptr_ohat < (uint64_t)(splits * rows * row_bytes)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_ohat: buffer ptr_ohat smaller than declared allocation");
     if (sz->ptr_lse < (uint64_t)(splits * rows * 4)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_lse: buffer ptr_lse smaller than declared allocation");
     if ((rc = rules_range(a, err, errlen)) != FMHA_OK) return rc;
-    if (splits < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x280) outside contract");
+    if (splits < 1 || (ka->kvs_splits & ~(0xffffu | FMHA_KVS_F32_PARTIALS)) != 0)
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x280) outside contract");
     if (rows < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x284) outside contract");
     if ((rc = rules_is(a, HK, err, errlen)) != FMHA_OK) return rc;
     if (rows != B * (i64)a.s_seq_len * (i64)a.s_q_head_num) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0x284) relation failed");
@@ -210,13 +213,14 @@ int fmha_mxfp8_validate_combine(const fmha_mxfp8_combine_args* a, const fmha_mxf
                                 uint32_t gy, uint32_t gz, char* err, size_t errlen) {
     // combine8h_abi.h:56-65
     (void)gx; (void)gy; (void)gz;
-    const i64 rows = a->rows_total, splits = a->splits;
+    const i64 rows = a->rows_total, splits = a->splits & 0xffffu;
     if (sz->ptr_ohat < (uint64_t)(splits * rows * 512)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_ohat: buffer ptr_ohat smaller than declared allocation");
     if (sz->ptr_lse < (uint64_t)(splits * rows * 4)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_lse: buffer ptr_lse smaller than declared allocation");
     if (sz->ptr_o < (uint64_t)(rows * 256)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_out: buffer ptr_out smaller than declared allocation");
     if (rows < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x18) outside contract");
     if (a->d != 128) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x1C) outside contract");
-    if (splits < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x20) outside contract");
+    if (splits < 1 || (a->splits & ~(0xffffu | FMHA_KVS_F32_PARTIALS)) != 0)
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x20) outside contract");
     return FMHA_OK;
 }
 
@@ -314,6 +318,8 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
         if (empty_split(SK, splits)) return fail(err, errlen, FMHA_ERR_PATH, "GV-HOST-PATH", "KV split leaves a split without a key tile");
         if (p->causal) return fail(err, errlen, FMHA_ERR_PATH, "GV-HOST-PATH", "the causal mask is not supported on the KV-split path");
     }
+    if (p->f32_partials != 0 && p->f32_partials != 1)
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "f32_partials must be 0 or 1");
     fmha_mxfp8_args a;
     fmha_mxfp8_fill_args(&a, p->o, p->q, p->k, p->v, p->q_descale, p->k_descale, p->v_descale, (int)B, (int)H, (int)HK, (int)S, (int)SK);
     a.flags = p->causal ? 1u : 0u;
@@ -347,7 +353,8 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     std::memcpy(&ka, &a, 0x270);
     ka.ptr_ohat = ohat;
     ka.ptr_lse = lse;
-    ka.kvs_splits = (uint32_t)splits;
+    const uint32_t part_fmt = p->f32_partials ? FMHA_KVS_F32_PARTIALS : 0u;
+    ka.kvs_splits = (uint32_t)splits | part_fmt;
     ka.kvs_rows_total = (uint32_t)rows_total;
     sz.ptr_ohat = (uint64_t)splits * rows_total * 512;
     sz.ptr_lse = (uint64_t)splits * rows_total * 4;
@@ -362,7 +369,7 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     ca.ptr_out = p->o;
     ca.rows_total = (uint32_t)rows_total;
     ca.d = 128;
-    ca.splits = (uint32_t)splits;
+    ca.splits = (uint32_t)splits | part_fmt;
     fmha_mxfp8_buffer_sizes csz = sz;
     csz.ptr_o = p->bytes_o;
     rc = fmha_mxfp8_validate_combine(&ca, &csz, 0, 1, 1, err, errlen);

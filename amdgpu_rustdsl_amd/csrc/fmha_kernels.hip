@@ -75,6 +75,7 @@ struct Prm {
     uint8_t* ohat;
     float* lse;
     uint32_t splits, rows_total;
+    uint32_t f32_partials;   // kvsplit extension: partial rows as f32 (512 B) instead of fp16 (256 B)
 #ifdef FMHA_TRACE
     uint64_t* trace;   // debug builds only: per (block, wave) timestamps, pointer at kernarg 0x288
     uint64_t t_entry;  // timestamp of the kernel's first instruction
@@ -136,7 +137,7 @@ __device__ inline Prm prm_from_kernarg() {
     p.k_b = KA_FIELD(uint32_t, s_k_Bs); p.v_seq = KA_FIELD(uint32_t, s_v_Seqs); p.v_b = KA_FIELD(uint32_t, s_v_Bs);
     p.o_seq = KA_FIELD(uint32_t, s_o_Seqs); p.o_b = KA_FIELD(uint32_t, s_o_Bs);
     p.qs_b = KA_FIELD(uint32_t, s_descale_q_Bs); p.ks_b = KA_FIELD(uint32_t, s_descale_k_Bs);
-    p.ohat = nullptr; p.lse = nullptr; p.splits = 1; p.rows_total = 0;
+    p.ohat = nullptr; p.lse = nullptr; p.splits = 1; p.rows_total = 0; p.f32_partials = 0;
 #ifdef FMHA_TRACE
     p.trace = (uint64_t*)(uintptr_t)(ka<uint32_t>(0x288) | ((uint64_t)ka<uint32_t>(0x28C) << 32));
 #endif
@@ -720,20 +721,34 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
         const float l_total = l * 0.0625f;
         const float fin = l > 0.0f ? __builtin_amdgcn_rcpf(l_total) * w.vd : 0.0f;
         const size_t prow = (size_t)split * p.rows_total + ((size_t)bidx * p.S + row) * p.H + head;
-        uint8_t* orow = p.ohat + prow * 256u;
+        if (p.f32_partials) {
+            // extension: f32 rows of 512 B (the workspace's rows are fp32-sized either way)
+            uint8_t* orow = p.ohat + prow * 512u;
 #pragma unroll
-        for (int dc = 0; dc < 4; ++dc)
+            for (int dc = 0; dc < 4; ++dc)
 #pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                uint32_t wd[2];
+                for (int a = 0; a < 4; ++a) {
+                    v4f x;
 #pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const uint32_t lo16 = f2h((w.o[dc][4 * a + 2 * c] * 0.0625f) * fin);
-                    const uint32_t hi16 = f2h((w.o[dc][4 * a + 2 * c + 1] * 0.0625f) * fin);
-                    wd[c] = lo16 | (hi16 << 16);
+                    for (int e = 0; e < 4; ++e) x[e] = (w.o[dc][4 * a + e] * 0.0625f) * fin;
+                    *(v4f*)(orow + (32 * dc + 8 * a + dbase) * 4) = x;
                 }
-                *(v2i*)(orow + (32 * dc + 8 * a + dbase) * 2) = (v2i){(int)wd[0], (int)wd[1]};
-            }
+        } else {
+            uint8_t* orow = p.ohat + prow * 256u;
+#pragma unroll
+            for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+                for (int a = 0; a < 4; ++a) {
+                    uint32_t wd[2];
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) {
+                        const uint32_t lo16 = f2h((w.o[dc][4 * a + 2 * c] * 0.0625f) * fin);
+                        const uint32_t hi16 = f2h((w.o[dc][4 * a + 2 * c + 1] * 0.0625f) * fin);
+                        wd[c] = lo16 | (hi16 << 16);
+                    }
+                    *(v2i*)(orow + (32 * dc + 8 * a + dbase) * 2) = (v2i){(int)wd[0], (int)wd[1]};
+                }
+        }
         if (hh == 0) {
             const float hl = h2f(w.bw) + h2f(w.bw >> 16);
             // an empty range (l = 0) gets -1e30: the combine gives it weight 0
@@ -1011,7 +1026,9 @@ extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvs
     p.lse_out = nullptr;
     p.ohat = (uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_kvsplit_args, ptr_ohat));
     p.lse = (float*)ka<uint64_t>(offsetof(fmha_mxfp8_kvsplit_args, ptr_lse));
-    p.splits = ka<uint32_t>(offsetof(fmha_mxfp8_kvsplit_args, kvs_splits));
+    const uint32_t split_field = ka<uint32_t>(offsetof(fmha_mxfp8_kvsplit_args, kvs_splits));
+    p.splits = split_field & 0xffffu;
+    p.f32_partials = (split_field & FMHA_KVS_F32_PARTIALS) ? 1u : 0u;
     p.rows_total = ka<uint32_t>(offsetof(fmha_mxfp8_kvsplit_args, kvs_rows_total));
     uint32_t qt, head, z;
     block_coords(p.S, p.H, 256u, qt, head, z);
@@ -1031,7 +1048,9 @@ extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvs
 extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvsplit_combine8h(fmha_mxfp8_combine_args a_) {
     (void)a_;
     const uint32_t rows = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, rows_total));
-    const uint32_t splits = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, splits));
+    const uint32_t split_field = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, splits));
+    const uint32_t splits = split_field & 0xffffu;
+    const bool f32 = (split_field & FMHA_KVS_F32_PARTIALS) != 0u;   // extension: f32 partial rows
     const uint32_t groups = rows << 4;
     uint32_t t = blockIdx.x * 256u + threadIdx.x;
     t = t < groups ? t : groups - 1u;
@@ -1045,17 +1064,23 @@ extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvspli
     for (uint32_t s = 0; s < splits; ++s) {
         const size_t rs = (size_t)s * rows;
         const float l = lse[rs + row];
-        const v4i ov = *(const v4i*)(ohat + ((rs << 4) + t) * 16u);
+        float x[8];
+        if (f32) {
+            const v4f x0 = *(const v4f*)(ohat + ((rs << 4) + t) * 32u), x1 = *(const v4f*)(ohat + ((rs << 4) + t) * 32u + 16u);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { x[i] = x0[i]; x[4 + i] = x1[i]; }
+        } else {
+            const v4i ov = *(const v4i*)(ohat + ((rs << 4) + t) * 16u);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { x[2 * i] = h2f((uint32_t)ov[i]); x[2 * i + 1] = h2f((uint32_t)ov[i] >> 16); }
+        }
         const float m_new = fmaxf(m, l);
         const float dm = m_new * -1.0f;
         const float al = __builtin_amdgcn_exp2f(m + dm);
         const float w = __builtin_amdgcn_exp2f(l + dm);
         den = den * al + w;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            acc[2 * i] = acc[2 * i] * al + w * h2f((uint32_t)ov[i]);
-            acc[2 * i + 1] = acc[2 * i + 1] * al + w * h2f((uint32_t)ov[i] >> 16);
-        }
+        for (int i = 0; i < 8; ++i) acc[i] = acc[i] * al + w * x[i];
         m = m_new;
     }
     const float rd = __builtin_amdgcn_rcpf(den);

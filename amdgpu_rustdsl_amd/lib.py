@@ -25,6 +25,7 @@ _L = ctypes.CDLL(LIB_PATH)
 FMHA_OK, FMHA_ERR_EXTENT, FMHA_ERR_KA_RANGE, FMHA_ERR_KA_IS, FMHA_ERR_GRID, FMHA_ERR_SYM = 0, 1, 2, 3, 4, 5
 FMHA_ERR_PATH, FMHA_ERR_WORKSPACE, FMHA_ERR_HIP, FMHA_ERR_NO_DEVICE = 6, 7, 8, 9
 PATH_VS128, PATH_T128, PATH_KVSPLIT = 0, 1, 2
+KVS_F32_PARTIALS = 0x10000   # include/fmha_mxfp8.h FMHA_KVS_F32_PARTIALS
 PATH_NAMES = {PATH_VS128: "vs128", PATH_T128: "t128", PATH_KVSPLIT: "kvsplit"}
 PATH_IDS = {v: k for k, v in PATH_NAMES.items()}
 
@@ -74,7 +75,8 @@ class Params(ctypes.Structure):
                 ("lse", _vp), ("bytes_q", _u64), ("bytes_k", _u64), ("bytes_v", _u64), ("bytes_o", _u64),
                 ("bytes_q_descale", _u64), ("bytes_k_descale", _u64), ("bytes_v_descale", _u64),
                 ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("HK", ctypes.c_int32), ("S", ctypes.c_int32), ("SK", ctypes.c_int32),
-                ("path", ctypes.c_int32), ("splits", ctypes.c_int32), ("causal", ctypes.c_int32)]
+                ("path", ctypes.c_int32), ("splits", ctypes.c_int32), ("causal", ctypes.c_int32),
+                ("f32_partials", ctypes.c_int32)]
 
 
 assert ctypes.sizeof(Args) == 656 and ctypes.sizeof(KvsplitArgs) == 648 and ctypes.sizeof(CombineArgs) == 36

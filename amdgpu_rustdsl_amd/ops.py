@@ -52,7 +52,8 @@ def _ws(device, stream, nbytes):
     return buf
 
 
-def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", splits=None, stream=None, lse=None, causal=False):
+def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", splits=None, stream=None, lse=None, causal=False,
+                   partials="fp16"):
     """MXFP8 attention forward, head dim 128 (``out = softmax(q k^T) v`` in base 2 with the E8M0 1x32 scales).
 
     q        [B, S, H, 128]   fp8 e4m3 (uint8 or float8_e4m3fn)   k, v [B, SK, HK, 128] (H = gqa HK, gqa a power of two <= 16)
@@ -62,8 +63,11 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     out      [B, S, H, 128]   bf16
     path: "auto" | "vs128" | "t128" | "kvsplit" (``splits`` in {2, 4, 8}). Returns (path, splits).
     Extensions (not in the reference): ``lse`` [B, H, S] f32 receives the natural-log LSE (vs128 / t128);
-    ``causal`` applies the bottom-right causal mask (key t visible to query i iff t <= i + SK - S).
+    ``causal`` applies the bottom-right causal mask (key t visible to query i iff t <= i + SK - S);
+    ``partials="fp32"`` keeps the KV split's partial rows in f32 instead of the reference's fp16.
     """
+    if partials not in ("fp16", "fp32"):
+        raise ValueError(f"fmha_fwd_mxfp8: partials must be 'fp16' or 'fp32', got {partials!r}")
     B, S, H, d = q.shape
     _, SK, HK, _ = k.shape
     if d != D or k.shape[3] != D or H % HK or (H // HK) & (H // HK - 1) or H // HK > 16:
@@ -98,6 +102,7 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     p.bytes_q_descale, p.bytes_k_descale, p.bytes_v_descale = _cap(q_scale), _cap(k_scale), _cap(v_scale)
     p.B, p.H, p.HK, p.S, p.SK = B, H, HK, S, SK
     p.path, p.splits, p.causal = path_id, nsplit, int(bool(causal))
+    p.f32_partials = int(partials == "fp32")
     # the workspace only matters for the KV split; size it for the split the dispatch will choose
     want_path, want_splits = (select_path(B, H, S, SK) if path_id < 0 else (path, nsplit))
     ws, ws_bytes = None, 0

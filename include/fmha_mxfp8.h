@@ -108,9 +108,10 @@ typedef struct fmha_mxfp8_args {
  * (tests/gpu/generated/fmha_fwd_hd128_mxfp8_v3_kvsplit_abi.h, offsets 0x270-0x284). */
 typedef struct fmha_mxfp8_kvsplit_args {
     uint8_t base[0x270];      /* fmha_mxfp8_args bytes 0x000..0x26F */
-    void* ptr_ohat;           /* 0x270 fp16 partial rows, 256 B each, split stride rows_total*256 B */
+    void* ptr_ohat;           /* 0x270 fp16 partial rows, 256 B each, split stride rows_total*256 B
+                                 (FMHA_KVS_F32_PARTIALS: f32 rows, 512 B each, split stride rows_total*512 B) */
     void* ptr_lse;            /* 0x278 f32 base-2 LSE per partial row */
-    uint32_t kvs_splits;      /* 0x280 2, 4 or 8 */
+    uint32_t kvs_splits;      /* 0x280 2, 4 or 8, optionally OR FMHA_KVS_F32_PARTIALS */
     uint32_t kvs_rows_total;  /* 0x284 B*S*H */
 } fmha_mxfp8_kvsplit_args;
 
@@ -123,9 +124,15 @@ typedef struct fmha_mxfp8_combine_args {
     void* ptr_out;            /* 0x10 bf16 [rows_total,128] */
     uint32_t rows_total;      /* 0x18 */
     uint32_t d;               /* 0x1C 128 */
-    uint32_t splits;          /* 0x20 */
+    uint32_t splits;          /* 0x20 optionally OR FMHA_KVS_F32_PARTIALS */
 } fmha_mxfp8_combine_args;
 #pragma pack(pop)
+
+/* Extension (no counterpart in the reference, whose partials are fp16: block3.rs:334-336): OR-ed into kvs_splits
+ * (kvsplit 0x280) and into splits (combine 0x20), it makes the split kernel write its partial rows as f32 (512 B,
+ * filling the fp32-sized rows the workspace already has) and the combine read them so. The split count is the low
+ * 16 bits of either field; a launcher that follows the reference never sets bit 16. */
+#define FMHA_KVS_F32_PARTIALS 0x10000u
 
 /* Byte sizes of the caller's allocations, checked by the validate calls
  * (the reference's BufferSizes, ..._vs128_abi.h:131-139). */
@@ -212,6 +219,7 @@ typedef struct fmha_mxfp8_params {
     int32_t path;              /* -1 = auto (dispatch rule), else FMHA_PATH_* */
     int32_t splits;            /* KV split count when path == FMHA_PATH_KVSPLIT (2, 4 or 8; 0 = 4) */
     int32_t causal;            /* 0 = the reference semantics; 1 = bottom-right causal mask (extension) */
+    int32_t f32_partials;      /* KV split only: 0 = fp16 partial rows (the reference's); 1 = f32 (extension) */
 } fmha_mxfp8_params;
 
 /* fmha_fwd_hd128_mxfp8_auto: dispatch + validate + launch (+ combine), all on

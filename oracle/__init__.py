@@ -75,6 +75,10 @@ def lib():
         L.mxo_emulate.argtypes = [ctypes.POINTER(Problem), i, i, vp, vp, vp, i]
         L.mxo_combine.restype = None
         L.mxo_combine.argtypes = [vp, vp, vp, ctypes.c_long, i]
+        L.mxo_emulate_ex.restype = None
+        L.mxo_emulate_ex.argtypes = [ctypes.POINTER(Problem), i, i, vp, vp, vp, i, i]
+        L.mxo_combine_f32.restype = None
+        L.mxo_combine_f32.argtypes = [vp, vp, vp, ctypes.c_long, i]
         L.mxo_quant_rows_bf16.argtypes = [vp, ctypes.c_long, f, vp, vp]
         L.mxo_quant_rows_bf16.restype = None
         L.mxo_quant_tensor_bf16.argtypes = [vp, ctypes.c_long, vp]
@@ -127,17 +131,19 @@ def check_fp64(inp, out_bf16, rows=64, threads=0):
     return lib().mxo_check_fp64(ctypes.byref(p), _ptr(out), int(rows), int(threads)).as_dict()
 
 
-def emulate(inp, splits=0, rows=64, threads=0, partials=False):
+def emulate(inp, splits=0, rows=64, threads=0, partials=False, f32_partials=False):
     """Bit-level model of the reference kernels on the first ``rows`` rows of every (b, h).
-    Returns the bf16 output (uint16, rows not emulated are 0), and with ``partials`` also (ohat fp16, lse f32)."""
+    Returns the bf16 output (uint16, rows not emulated are 0), and with ``partials`` also (ohat, lse f32): ohat fp16
+    (uint16), or f32 with ``f32_partials`` (the FMHA_KVS_F32_PARTIALS extension)."""
     out = np.zeros(inp.out_elems, np.uint16)
     ohat = lse = None
     if partials and splits:
         rows_total = inp.B * inp.S * inp.H
-        ohat = np.zeros(splits * rows_total * D, np.uint16)
+        ohat = np.zeros(splits * rows_total * D, np.float32 if f32_partials else np.uint16)
         lse = np.zeros(splits * rows_total, np.float32)
     p = inp.problem()
-    lib().mxo_emulate(ctypes.byref(p), int(splits), int(rows), _ptr(out), _ptr(ohat), _ptr(lse), int(threads))
+    lib().mxo_emulate_ex(ctypes.byref(p), int(splits), int(rows), _ptr(out), _ptr(ohat), _ptr(lse), int(bool(f32_partials)),
+                         int(threads))
     return (out, ohat, lse) if partials else out
 
 
@@ -162,9 +168,14 @@ def split_range(SK, splits, s):
 
 
 def combine(ohat, lse, rows_total, splits):
+    """The combine on partial rows: fp16 (uint16 array) or, for a float32 array, f32 rows (the extension)."""
     out = np.zeros(rows_total * D, np.uint16)
-    lib().mxo_combine(_ptr(np.ascontiguousarray(ohat, np.uint16)), _ptr(np.ascontiguousarray(lse, np.float32)), _ptr(out),
-                      rows_total, splits)
+    if np.asarray(ohat).dtype == np.float32:
+        lib().mxo_combine_f32(_ptr(np.ascontiguousarray(ohat, np.float32)), _ptr(np.ascontiguousarray(lse, np.float32)),
+                              _ptr(out), rows_total, splits)
+    else:
+        lib().mxo_combine(_ptr(np.ascontiguousarray(ohat, np.uint16)), _ptr(np.ascontiguousarray(lse, np.float32)), _ptr(out),
+                          rows_total, splits)
     return out
 
 

@@ -574,8 +574,9 @@ typedef struct {
     const mxo_problem* p;
     int splits, rows;
     uint16_t* out;
-    uint16_t* ohat;
+    void* ohat;          /* fp16 rows, or f32 rows when f32_partials */
     float* lse;
+    int f32_partials;
 } emu_ctx;
 
 static void emu_item(const void* vctx, long item) {
@@ -605,7 +606,7 @@ static void emu_item(const void* vctx, long item) {
     const long rows_total = (long)p->B * p->S * p->H;
     const long prow = ((long)b * p->S + i) * p->H + h;
     float lse_s[8];
-    uint16_t oh[8][D];
+    float oh[8][D];      /* the partial row as stored (fp16-rounded unless f32_partials) */
     for (int s = 0; s < c->splits; ++s) {
         int key_lo, kv_eff;
         mxo_split_range(p->SK, c->splits, s, &key_lo, &kv_eff);
@@ -614,11 +615,22 @@ static void emu_item(const void* vctx, long item) {
          * with l_total = l / 16 (softmax.rs:277-305): the scaled PV form accumulates O / 16 */
         const float l_total = st.l * 0.0625f;
         const float fin = st.l > 0.0f ? (1.0f / l_total) * vd : 0.0f;
-        for (int d = 0; d < D; ++d) oh[s][d] = mxo_f32_to_f16((st.o[d] * 0.0625f) * fin);
+        for (int d = 0; d < D; ++d) {
+            const float x = (st.o[d] * 0.0625f) * fin;
+            /* extension: f32 partial rows keep x; the reference's fp16 rows round it (block3.rs:334-336) */
+            oh[s][d] = c->f32_partials ? x : mxo_f16_to_f32(mxo_f32_to_f16(x));
+        }
         const float hl = mxo_f16_to_f32((uint16_t)(st.w & 0xffff)) + mxo_f16_to_f32((uint16_t)(st.w >> 16));
         /* a split without keys gets lse -1e30: weight 0 in the combine */
         lse_s[s] = st.l > 0.0f ? log2f(l_total) + (hl * 2048.0f) * -1.0f : -1.0e30f;
-        if (c->ohat) memcpy(c->ohat + ((size_t)s * rows_total + prow) * D, oh[s], 2 * D);
+        if (c->ohat) {
+            if (c->f32_partials) {
+                memcpy((float*)c->ohat + ((size_t)s * rows_total + prow) * D, oh[s], 4 * D);
+            } else {
+                uint16_t* dst = (uint16_t*)c->ohat + ((size_t)s * rows_total + prow) * D;
+                for (int d = 0; d < D; ++d) dst[d] = mxo_f32_to_f16(oh[s][d]);
+            }
+        }
         if (c->lse) c->lse[(size_t)s * rows_total + prow] = lse_s[s];
     }
     /* combine (epilogue.rs:89-167) */
@@ -630,18 +642,43 @@ static void emu_item(const void* vctx, long item) {
         const float dm = m_new * -1.0f;
         const float a = exp2f(m + dm), w = exp2f(l + dm);
         den = den * a + w;
-        for (int d = 0; d < D; ++d) acc[d] = acc[d] * a + w * mxo_f16_to_f32(oh[s][d]);
+        for (int d = 0; d < D; ++d) acc[d] = acc[d] * a + w * oh[s][d];
         m = m_new;
     }
     const float rd = 1.0f / den;
     for (int d = 0; d < D; ++d) orow[d] = mxo_f32_to_bf16(acc[d] * rd);
 }
 
+void mxo_emulate_ex(const mxo_problem* p, int splits, int rows, uint16_t* out_bf16, void* ohat, float* lse_f32,
+                    int f32_partials, int threads) {
+    if (rows <= 0 || rows > p->S) rows = p->S;
+    emu_ctx c = {p, splits, rows, out_bf16, ohat, lse_f32, f32_partials};
+    run_parallel(threads, (long)p->B * p->H * rows, &c, emu_item);
+}
+
 void mxo_emulate(const mxo_problem* p, int splits, int rows, uint16_t* out_bf16,
                  uint16_t* ohat_f16, float* lse_f32, int threads) {
-    if (rows <= 0 || rows > p->S) rows = p->S;
-    emu_ctx c = {p, splits, rows, out_bf16, ohat_f16, lse_f32};
-    run_parallel(threads, (long)p->B * p->H * rows, &c, emu_item);
+    mxo_emulate_ex(p, splits, rows, out_bf16, ohat_f16, lse_f32, 0, threads);
+}
+
+/* The combine on f32 partial rows (the FMHA_KVS_F32_PARTIALS extension): the same arithmetic, no fp16 decode. */
+void mxo_combine_f32(const float* ohat_f32, const float* lse, uint16_t* out_bf16, long rows_total, int splits) {
+    for (long r = 0; r < rows_total; ++r) {
+        float m = -1.0e30f, den = 0.0f, acc[D];
+        for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+        for (int s = 0; s < splits; ++s) {
+            const float l = lse[(size_t)s * rows_total + r];
+            const float m_new = fmaxf(m, l);
+            const float dm = m_new * -1.0f;
+            const float a = exp2f(m + dm), w = exp2f(l + dm);
+            den = den * a + w;
+            const float* o = ohat_f32 + ((size_t)s * rows_total + r) * D;
+            for (int d = 0; d < D; ++d) acc[d] = acc[d] * a + w * o[d];
+            m = m_new;
+        }
+        const float rd = 1.0f / den;
+        for (int d = 0; d < D; ++d) out_bf16[(size_t)r * D + d] = mxo_f32_to_bf16(acc[d] * rd);
+    }
 }
 
 void mxo_combine(const uint16_t* ohat_f16, const float* lse, uint16_t* out_bf16, long rows_total, int splits) {

@@ -107,6 +107,13 @@ void mxo_emulate(const mxo_problem* p, int splits, int rows, uint16_t* out_bf16,
 /* The combine kernel's arithmetic on given partials (epilogue.rs:89-167). */
 void mxo_combine(const uint16_t* ohat_f16, const float* lse, uint16_t* out_bf16, long rows_total, int splits);
 
+/* Extension (no reference counterpart): mxo_emulate with the KV split's partial rows kept in f32 when f32_partials
+ * (ohat then receives f32 rows), and the combine on f32 partial rows. The fp16 path of mxo_emulate is
+ * mxo_emulate_ex(..., 0, ...). */
+void mxo_emulate_ex(const mxo_problem* p, int splits, int rows, uint16_t* out_bf16, void* ohat, float* lse_f32,
+                    int f32_partials, int threads);
+void mxo_combine_f32(const float* ohat_f32, const float* lse, uint16_t* out_bf16, long rows_total, int splits);
+
 #ifdef __cplusplus
 }
 #endif

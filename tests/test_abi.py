@@ -150,6 +150,22 @@ def test_validate_kvsplit():
     assert lib.validate("kvsplit", ka, sz, g, B=1, HK=8, KL=-1)[0] == lib.FMHA_ERR_SYM
 
 
+def test_validate_f32_partials_flag():
+    """The f32-partials extension rides in bit 16 of the split fields (kvsplit 0x280, combine 0x20): accepted with the
+    split count in the low 16 bits, which the grid relation uses; any other high bit is out of contract."""
+    ka, sz, g = _kvsplit()
+    ka.kvs_splits = 8 | lib.KVS_F32_PARTIALS
+    assert lib.validate("kvsplit", ka, sz, g, B=1, HK=8, KL=0) == (0, "")
+    ka.kvs_splits = 8 | (1 << 17)
+    rc, msg = lib.validate("kvsplit", ka, sz, g, B=1, HK=8)
+    assert rc == lib.FMHA_ERR_KA_RANGE and "0x280" in msg
+    ca = lib.CombineArgs(0x1, 0x2, 0x3, 1024, 128, 8 | lib.KVS_F32_PARTIALS)
+    csz = lib.BufferSizes(0, 0, 0, 1024 * 256, 0, 0, 0, 8 * 1024 * 512, 8 * 1024 * 4)
+    assert lib.validate("combine", ca, csz, (64, 1, 1)) == (0, "")
+    ca.splits = 8 | (1 << 20)
+    assert lib.validate("combine", ca, csz, (64, 1, 1))[0] == lib.FMHA_ERR_KA_RANGE
+
+
 def test_validate_combine():
     ca = lib.CombineArgs(0x1, 0x2, 0x3, 1024, 128, 8)
     sz = lib.BufferSizes(0, 0, 0, 1024 * 256, 0, 0, 0, 8 * 1024 * 512, 8 * 1024 * 4)

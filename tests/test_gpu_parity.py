@@ -97,6 +97,38 @@ def test_parity_causal(gpu, case):
         assert (o[:, : S - SK] == 0).all()   # query i sees keys t <= i + SK - S: none for i < S - SK
 
 
+# Extension: the KV split with f32 partial rows (partials="fp32"; the reference writes fp16). Bar: the statistical one
+# against the oracle's emulation of the same variant, and no worse than the fp16 variant of the GPU path itself.
+F32_CASES = [
+    ("cfg5_B1H8S128_SK16384_split8", 1, 8, 8, 128, 16384, 8),
+    ("cfg5_B1H8S128_SK16000_split8", 1, 8, 8, 128, 16000, 8),
+    ("gqa4_B1H8HK2_S2048_split4", 1, 8, 2, 2048, 2048, 4),
+    ("split2_B1H4S300_SK1000", 1, 4, 4, 300, 1000, 2),
+]
+
+
+@pytest.mark.parametrize("case", F32_CASES, ids=[c[0] for c in F32_CASES])
+def test_parity_f32_partials(gpu, case):
+    name, B, H, HK, S, SK, splits = case
+    print(f"[case] f32 partials {name}", flush=True)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK)
+    out, used, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits, partials="fp32")
+    assert used == ("kvsplit", splits)
+    out16, _, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits)
+    emu = oracle.emulate(inp, splits=splits, rows=ROWS, f32_partials=True)
+    ref_stats = oracle.check_fp64(inp, emu, rows=ROWS)
+    stats = oracle.check_fp64(inp, out, rows=ROWS)
+    stats16 = oracle.check_fp64(inp, out16, rows=ROWS)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, min(ROWS, S))
+    print(f"[case] f32 partials {name} ours={stats} fp16-partials={stats16} emulated={ref_stats} vs-emulation={cmp}", flush=True)
+    assert not np.isnan(oracle.bf16_to_f32(out)).any()
+    assert stats["bad"] <= ref_stats["bad"]
+    assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"]
+    assert stats["mean_err"] <= stats16["mean_err"] * 1.01
+    assert cmp["mean_abs"] <= 0.6 * ref_stats["mean_err"], cmp
+    assert cmp["max_abs"] <= 0.05, cmp
+
+
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("shape", [(1, 4, 4, 512, 640), (4, 8, 8, 1024, 1024)], ids=["t128", "vs128"])
 def test_lse_output(gpu, shape, causal):

@@ -344,6 +344,41 @@ def test_emulated_partials_combine_to_emulated_output():
     np.testing.assert_array_equal(merged, out)
 
 
+def test_combine_f32_closed_form():
+    """The combine on f32 partial rows (extension) is the same streaming merge: the closed form to bf16 rounding, and
+    on fp16-representable rows it equals the fp16 combine bit for bit."""
+    rng = np.random.default_rng(12)
+    rows, splits = 29, 8
+    ohat = rng.standard_normal((splits, rows, D)).astype(np.float32)
+    lse = (rng.standard_normal((splits, rows)) * 6 - 3).astype(np.float32)
+    lse[3, 7] = -1e30
+    out = oracle.bf16_to_f32(oracle.combine(ohat, lse, rows, splits)).reshape(rows, D).astype(np.float64)
+    w = np.exp2(lse.astype(np.float64) - lse.max(0))
+    w[lse < -1e29] = 0.0
+    ref = (w[:, :, None] * ohat.astype(np.float64)).sum(0) / w.sum(0)[:, None]
+    assert (np.abs(out - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6).all()
+    h = ohat.astype(np.float16)
+    np.testing.assert_array_equal(oracle.combine(h.astype(np.float32), lse, rows, splits),
+                                  oracle.combine(h.view(np.uint16), lse, rows, splits))
+
+
+def test_emulated_f32_partials():
+    """Emulated KV split with f32 partial rows (extension): the rows are the fp16 rows before their rounding (within
+    one fp16 rounding step), they combine to the emulated output bit for bit, and the result is at least as close to
+    fp64 attention as the fp16 path."""
+    inp = oracle.Inputs(1, 2, 40, 1000)
+    splits = 4
+    out16, oh16, lse16 = oracle.emulate(inp, splits=splits, rows=0, partials=True)
+    out32, oh32, lse32 = oracle.emulate(inp, splits=splits, rows=0, partials=True, f32_partials=True)
+    np.testing.assert_array_equal(lse16, lse32)
+    assert oh32.dtype == np.float32
+    np.testing.assert_array_equal(oh32.astype(np.float16).view(np.uint16), oh16)
+    np.testing.assert_array_equal(oracle.combine(oh32, lse32, inp.B * inp.S * inp.H, splits), out32)
+    e16 = oracle.check_fp64(inp, out16, rows=inp.S)
+    e32 = oracle.check_fp64(inp, out32, rows=inp.S)
+    assert e32["bad"] <= e16["bad"] and e32["mean_err"] <= e16["mean_err"] * 1.01
+
+
 # ------------------------------------------------------------------ quantisers of bf16 inputs
 
 _E4M3 = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
