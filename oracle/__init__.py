@@ -26,7 +26,8 @@ def build():
 class Problem(ctypes.Structure):
     _fields_ = [("B", ctypes.c_int), ("H", ctypes.c_int), ("HK", ctypes.c_int), ("S", ctypes.c_int), ("SK", ctypes.c_int),
                 ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
-                ("qs", ctypes.c_void_p), ("ks", ctypes.c_void_p), ("vdescale", ctypes.c_float), ("causal", ctypes.c_int)]
+                ("qs", ctypes.c_void_p), ("ks", ctypes.c_void_p), ("vdescale", ctypes.c_float), ("causal", ctypes.c_int),
+                ("vs32", ctypes.c_void_p)]
 
 
 class CheckResult(ctypes.Structure):
@@ -99,7 +100,7 @@ MODES = {"lcg": 0, "uniform": 1, "normal": 2}
 class Inputs:
     """Seeded MXFP8 inputs in the reference layout (ref_host.cpp:183-263), host numpy arrays."""
 
-    def __init__(self, B, H, S, SK, HK=None, mode="normal", seed_mix=0, causal=False):
+    def __init__(self, B, H, S, SK, HK=None, mode="normal", seed_mix=0, causal=False, v_seq32=False):
         HK = HK or H
         self.B, self.H, self.HK, self.S, self.SK, self.causal = B, H, HK, S, SK, bool(causal)
         L = lib()
@@ -112,10 +113,20 @@ class Inputs:
                                              _ptr(self.v), _ptr(self.qs), _ptr(self.ks)))
         self.vd_buf = np.zeros(1024, np.float32)
         self.vd_buf[0] = self.vdescale
+        self.vs32 = None
+        if v_seq32:
+            # extension: V re-quantised with one E8M0 per 32 keys per column (the seq32 rule) from the generator's V,
+            # dequantised and rounded to bf16; the FMHA then reads the scales instead of the f32 descale
+            dec = np.array([L.mxo_e4m3_decode(i) for i in range(256)], np.float32)
+            vals = dec[self.v] * np.float32(self.vdescale)
+            u = vals.view(np.uint32)
+            bf = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)    # f32 -> bf16, round to nearest even
+            self.v, self.vs32 = quant_seq32_bf16(bf, B, SK, HK)
 
     def problem(self):
         p = Problem(self.B, self.H, self.HK, self.S, self.SK, _ptr(self.q).value, _ptr(self.k).value, _ptr(self.v).value,
-                    _ptr(self.qs).value, _ptr(self.ks).value, self.vdescale, int(self.causal))
+                    _ptr(self.qs).value, _ptr(self.ks).value, self.vdescale, int(self.causal),
+                    _ptr(self.vs32).value if self.vs32 is not None else None)
         return p
 
     @property

@@ -28,6 +28,15 @@
 
 #define D 128
 
+/* V element scale: 2^(E8M0 - 127) of its 32-key block and column under per-32 V scales (extension), else 1 */
+static inline double v_block_scale(const mxo_problem* p, int b, int key, int kvh, int d) {
+    if (!p->vs32) return 1.0;
+    const size_t nb = ((size_t)p->SK + 31) / 32;
+    return ldexp(1.0, (int)p->vs32[(((size_t)b * nb + (size_t)key / 32) * p->HK + kvh) * D + d] - 127);
+}
+/* the per-tensor V descale the output is multiplied by (1 under per-32 V scales) */
+static inline float v_tensor_descale(const mxo_problem* p) { return p->vs32 ? 1.0f : p->vdescale; }
+
 /* ------------------------------------------------------------------ scalars */
 
 double mxo_e4m3_decode(uint8_t b) {
@@ -337,8 +346,9 @@ static void check_item(const void* vctx, long item) {
         for (int t = 0; t < nvis; ++t) { sc[t] = exp(sc[t] - mx); den += sc[t]; }
         for (int d = 0; d < D; ++d) {
             double acc = 0.0;
-            for (int t = 0; t < nvis; ++t) acc += sc[t] / den * mxo_e4m3_decode(p->v[(((size_t)b * p->SK + t) * p->HK + kvh) * D + d]);
-            acc *= p->vdescale;
+            for (int t = 0; t < nvis; ++t)
+                acc += sc[t] / den * mxo_e4m3_decode(p->v[(((size_t)b * p->SK + t) * p->HK + kvh) * D + d]) * v_block_scale(p, b, t, kvh, d);
+            acc *= v_tensor_descale(p);
             const double got = mxo_bf16_to_f32(c->o[(((size_t)b * p->S + i) * p->H + h) * D + d]);
             const double err = fabs(got - acc);
             if (err != err) worst = INFINITY; else worst = fmax(worst, err);
@@ -433,7 +443,10 @@ double mxo_attention_fp32(const mxo_problem* p, int rows, float* out_f32, int th
     float* vf = (float*)malloc(nk * 4);
     for (size_t i = 0; i < nq; ++i) qf[i] = (float)(mxo_e4m3_decode(p->q[i]) * ldexp(1.0, (int)p->qs[i / 32] - 127));
     for (size_t i = 0; i < nk; ++i) kf[i] = (float)(mxo_e4m3_decode(p->k[i]) * ldexp(1.0, (int)p->ks[i / 32] - 127));
-    for (size_t i = 0; i < nk; ++i) vf[i] = (float)mxo_e4m3_decode(p->v[i]) * p->vdescale;
+    for (size_t i = 0; i < nk; ++i) {
+        const int d = (int)(i % D), kvh = (int)(i / D % p->HK), key = (int)(i / D / p->HK % p->SK), b = (int)(i / D / p->HK / p->SK);
+        vf[i] = (float)(mxo_e4m3_decode(p->v[i]) * v_block_scale(p, b, key, kvh, d)) * v_tensor_descale(p);
+    }
     struct timespec t0, t1;
     clock_gettime(CLOCK_MONOTONIC, &t0);
     attn_ctx c = {p, qf, kf, vf, out_f32, rows, 16, 0};
@@ -563,7 +576,8 @@ static void emulate_row(const mxo_problem* p, const recipe_t* rc, int b, int kvh
                     if (!pb[j]) continue;
                     const int key = t0 + j;
                     const int kr = key < p->SK ? key : p->SK - 1;
-                    a += g_e4m3_val[pb[j]] * g_e4m3_val[p->v[(((size_t)b * p->SK + kr) * p->HK + kvh) * D + d]];
+                    a += g_e4m3_val[pb[j]] * g_e4m3_val[p->v[(((size_t)b * p->SK + kr) * p->HK + kvh) * D + d]] *
+                         v_block_scale(p, b, kr, kvh, d);
                 }
                 st->o[d] = (float)((double)st->o[d] + a);
             }
@@ -593,7 +607,7 @@ static void emu_item(const void* vctx, long item) {
     for (int d = 0; d < D; ++d) qv[d] = mxo_e4m3_decode(p->q[(((size_t)b * p->S + i) * p->H + h) * D + d]);
     for (int blk = 0; blk < 4; ++blk) sq[blk] = ((int)p->qs[(((size_t)b * p->S + i) * p->H + h) * 4 + blk] - 9) & 0xff;
     const int kvis = visible_keys(p, i);
-    const float vd = p->vdescale;
+    const float vd = v_tensor_descale(p);
     row_state st;
     uint16_t* orow = c->out + (((size_t)b * p->S + i) * p->H + h) * D;
     if (c->splits <= 0) {

@@ -40,6 +40,8 @@ typedef struct mxo_problem {
     const uint8_t* ks;  /* [B,SK,HK,4] E8M0 */
     float vdescale;
     int causal;         /* bottom-right causal mask: key t visible for query i iff t <= i + SK - S */
+    const uint8_t* vs32;/* extension: NULL = one f32 V descale (vdescale, the reference's); else E8M0 V scales
+                           [B, ceil(SK/32), HK, 128], one per 32 keys per column, and vdescale is not used */
 } mxo_problem;
 
 typedef struct mxo_check_result {

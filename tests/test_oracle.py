@@ -228,7 +228,11 @@ def _numpy_attention(inp, rows):
     B, H, HK, S, SK = inp.B, inp.H, inp.HK, inp.S, inp.SK
     q = dec[inp.q].reshape(B, S, H, 4, 32) * 2.0 ** (inp.qs[: B * S * H * 4].reshape(B, S, H, 4, 1).astype(np.float64) - 127)
     k = dec[inp.k].reshape(B, SK, HK, 4, 32) * 2.0 ** (inp.ks[: B * SK * HK * 4].reshape(B, SK, HK, 4, 1).astype(np.float64) - 127)
-    v = dec[inp.v].reshape(B, SK, HK, D) * inp.vdescale
+    if inp.vs32 is not None:   # extension: one E8M0 per 32 keys per column
+        vsc = 2.0 ** (inp.vs32.reshape(B, -1, HK, D).astype(np.float64) - 127)
+        v = dec[inp.v].reshape(B, SK, HK, D) * np.repeat(vsc, 32, axis=1)[:, :SK]
+    else:
+        v = dec[inp.v].reshape(B, SK, HK, D) * inp.vdescale
     q, k = q.reshape(B, S, H, D), k.reshape(B, SK, HK, D)
     g = H // HK
     out = np.zeros((B, rows, H, D))
@@ -244,11 +248,11 @@ def _numpy_attention(inp, rows):
     return out
 
 
-@pytest.mark.parametrize("causal", [False, True])
-def test_check_fp64_matches_numpy(causal):
+@pytest.mark.parametrize("causal,v_seq32", [(False, False), (True, False), (False, True)])
+def test_check_fp64_matches_numpy(causal, v_seq32):
     """ref_host.cpp:436-471 statistics (bad = |err| > 0.05 + 0.05 |ref|, mean |err|) of a given output == the same
-    statistics computed from numpy float64 attention."""
-    inp = oracle.Inputs(2, 4, 40, 70, HK=2, causal=causal)
+    statistics computed from numpy float64 attention (also with the per-32-key V scales of the extension)."""
+    inp = oracle.Inputs(2, 4, 40, 70, HK=2, causal=causal, v_seq32=v_seq32)
     rows = 24
     ref = _numpy_attention(inp, rows)
     rng = np.random.default_rng(1)
@@ -263,9 +267,9 @@ def test_check_fp64_matches_numpy(causal):
     assert abs(got["mean_err"] - err.mean()) <= 1e-9 * max(1.0, err.mean())
 
 
-@pytest.mark.parametrize("causal", [False, True])
-def test_attention_fp32_matches_numpy(causal):
-    inp = oracle.Inputs(1, 4, 50, 90, HK=4, causal=causal)
+@pytest.mark.parametrize("causal,v_seq32", [(False, False), (True, False), (False, True)])
+def test_attention_fp32_matches_numpy(causal, v_seq32):
+    inp = oracle.Inputs(1, 4, 50, 90, HK=4, causal=causal, v_seq32=v_seq32)
     _, out = oracle.attention_fp32(inp, rows=0)
     ref = _numpy_attention(inp, inp.S)
     np.testing.assert_allclose(out.reshape(ref.shape), ref, atol=2e-5, rtol=1e-4)
@@ -377,6 +381,28 @@ def test_emulated_f32_partials():
     e16 = oracle.check_fp64(inp, out16, rows=inp.S)
     e32 = oracle.check_fp64(inp, out32, rows=inp.S)
     assert e32["bad"] <= e16["bad"] and e32["mean_err"] <= e16["mean_err"] * 1.01
+
+
+def test_emulation_v_seq32_scales():
+    """Per-32-key V scales (extension) in the recipe emulation: raising every scale by one binade doubles the output
+    exactly; raising only block 1 of column 5 changes only column 5, and only for rows that see keys 32..63; the
+    statistics stay those of the per-tensor V (same data, re-quantised)."""
+    inp = oracle.Inputs(1, 2, 48, 100, v_seq32=True)
+    base = oracle.bf16_to_f32(oracle.emulate(inp, rows=0)).reshape(1, 48, 2, D)
+    keep = inp.vs32.copy()
+    inp.vs32 = keep + 1
+    np.testing.assert_array_equal(oracle.bf16_to_f32(oracle.emulate(inp, rows=0)).reshape(base.shape), 2 * base)
+    sc = keep.copy().reshape(1, -1, 2, D)
+    sc[:, 1, :, 5] += 1
+    inp.vs32 = sc.reshape(-1)
+    got = oracle.bf16_to_f32(oracle.emulate(inp, rows=0)).reshape(base.shape)
+    changed = got != base
+    assert changed[..., 5].any() and not np.delete(changed, 5, axis=-1).any()
+    inp.vs32 = keep
+    ref = oracle.Inputs(1, 2, 48, 100)
+    e32 = oracle.check_fp64(inp, oracle.emulate(inp, rows=0), rows=48)
+    et = oracle.check_fp64(ref, oracle.emulate(ref, rows=0), rows=48)
+    assert e32["bad"] == et["bad"] == 0 and 0.7 * et["mean_err"] < e32["mean_err"] < 1.4 * et["mean_err"]
 
 
 # ------------------------------------------------------------------ quantisers of bf16 inputs
