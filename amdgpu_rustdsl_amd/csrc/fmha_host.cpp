@@ -97,7 +97,8 @@ typedef long long i64;
 // The 0x000-0x26F rules shared by vs128 / t128 / kvsplit (vs128_abi.h:170-203), in the reference's four groups
 // and order: buffer extents, kernarg ranges, kernarg relations, grid. `B` is grid.z for the single-kernel launches
 // and the host symbol B for the KV split (kvsplit_abi.h).
-int rules_extent(const fmha_mxfp8_args& a, const fmha_mxfp8_buffer_sizes& sz, i64 B, char* err, size_t errlen) {
+// v_seq32: the per-32-key V-scale extension, whose ptr_v_descale holds E8M0 [B, ceil(SK/32), HK, 128]
+int rules_extent(const fmha_mxfp8_args& a, const fmha_mxfp8_buffer_sizes& sz, i64 B, bool v_seq32, char* err, size_t errlen) {
     const i64 H = a.s_q_head_num;
     if (sz.ptr_q < (uint64_t)(B * (i64)a.s_Bs)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_q: buffer ptr_q smaller than declared allocation");
     if (sz.ptr_k < (uint64_t)(B * (i64)a.s_k_Bs)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_k: buffer ptr_k smaller than declared allocation");
@@ -107,7 +108,8 @@ int rules_extent(const fmha_mxfp8_args& a, const fmha_mxfp8_buffer_sizes& sz, i6
         return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_q_descale: buffer ptr_q_descale smaller than declared allocation");
     if (sz.ptr_k_descale < (uint64_t)(B * (i64)a.s_descale_k_Bs + 2560LL * H))
         return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_k_descale: buffer ptr_k_descale smaller than declared allocation");
-    if (sz.ptr_v_descale < 4096ull) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_v_descale: buffer ptr_v_descale smaller than declared allocation");
+    const uint64_t vd_need = v_seq32 ? (uint64_t)(B * (((i64)a.s_kv_seq_len + 31) / 32) * (i64)a.s_k_Seqs) : 4096ull;
+    if (sz.ptr_v_descale < vd_need) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_v_descale: buffer ptr_v_descale smaller than declared allocation");
     return FMHA_OK;
 }
 
@@ -151,8 +153,10 @@ int rules_grid(const fmha_mxfp8_args& a, uint32_t gx, uint32_t gy, int rows_per_
 int validate_base(const fmha_mxfp8_args& a, const fmha_mxfp8_buffer_sizes& sz, uint32_t gx, uint32_t gy, i64 B, i64 HK,
                   int rows_per_block, char* err, size_t errlen) {
     int rc;
-    if ((rc = rules_extent(a, sz, B, err, errlen)) != FMHA_OK) return rc;
+    if ((rc = rules_extent(a, sz, B, (a.flags & FMHA_FLAG_V_SEQ32) != 0, err, errlen)) != FMHA_OK) return rc;
     if ((rc = rules_range(a, err, errlen)) != FMHA_OK) return rc;
+    if ((a.flags & ~(FMHA_FLAG_CAUSAL | FMHA_FLAG_V_SEQ32)) != 0)
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x280) outside contract");
     if ((rc = rules_is(a, HK, err, errlen)) != FMHA_OK) return rc;
     return rules_grid(a, gx, gy, rows_per_block, err, errlen);
 }
@@ -194,11 +198,11 @@ int fmha_mxfp8_validate_kvsplit(const fmha_mxfp8_kvsplit_args* ka, const fmha_mx
     const i64 splits = ka->kvs_splits & 0xffffu, rows = ka->kvs_rows_total;
     const i64 row_bytes = 512;   // the workspace rows are fp32-sized in both formats
     int rc;
-    if ((rc = rules_extent(a, *sz, B, err, errlen)) != FMHA_OK) return rc;
+    if ((rc = rules_extent(a, *sz, B, (ka->kvs_splits & FMHA_KVS_V_SEQ32) != 0, err, errlen)) != FMHA_OK) return rc;
     if (sz->ptr_ohat < (uint64_t)(splits * rows * row_bytes)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_ohat: buffer ptr_ohat smaller than declared allocation");
     if (sz->ptr_lse < (uint64_t)(splits * rows * 4)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_lse: buffer ptr_lse smaller than declared allocation");
     if ((rc = rules_range(a, err, errlen)) != FMHA_OK) return rc;
-    if (splits < 1 || (ka->kvs_splits & ~(0xffffu | FMHA_KVS_F32_PARTIALS)) != 0)
+    if (splits < 1 || (ka->kvs_splits & ~(0xffffu | FMHA_KVS_F32_PARTIALS | FMHA_KVS_V_SEQ32)) != 0)
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x280) outside contract");
     if (rows < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x284) outside contract");
     if ((rc = rules_is(a, HK, err, errlen)) != FMHA_OK) return rc;
@@ -320,9 +324,11 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     }
     if (p->f32_partials != 0 && p->f32_partials != 1)
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "f32_partials must be 0 or 1");
+    if (p->v_seq32 != 0 && p->v_seq32 != 1)
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "v_seq32 must be 0 or 1");
     fmha_mxfp8_args a;
     fmha_mxfp8_fill_args(&a, p->o, p->q, p->k, p->v, p->q_descale, p->k_descale, p->v_descale, (int)B, (int)H, (int)HK, (int)S, (int)SK);
-    a.flags = p->causal ? 1u : 0u;
+    a.flags = (p->causal ? FMHA_FLAG_CAUSAL : 0u) | (p->v_seq32 ? FMHA_FLAG_V_SEQ32 : 0u);
     fmha_mxfp8_buffer_sizes sz;
     std::memset(&sz, 0, sizeof(sz));
     sz.ptr_q = p->bytes_q; sz.ptr_k = p->bytes_k; sz.ptr_v = p->bytes_v; sz.ptr_o = p->bytes_o;
@@ -354,7 +360,7 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     ka.ptr_ohat = ohat;
     ka.ptr_lse = lse;
     const uint32_t part_fmt = p->f32_partials ? FMHA_KVS_F32_PARTIALS : 0u;
-    ka.kvs_splits = (uint32_t)splits | part_fmt;
+    ka.kvs_splits = (uint32_t)splits | part_fmt | (p->v_seq32 ? FMHA_KVS_V_SEQ32 : 0u);
     ka.kvs_rows_total = (uint32_t)rows_total;
     sz.ptr_ohat = (uint64_t)splits * rows_total * 512;
     sz.ptr_lse = (uint64_t)splits * rows_total * 4;

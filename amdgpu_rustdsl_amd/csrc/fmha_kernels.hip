@@ -59,7 +59,12 @@ constexpr int kLdsV = kSlots * kTileBytes;    // kSlots V tiles
 constexpr int kLdsKs = 2 * kSlots * kTileBytes;   // kSlots x 1 KiB of K scales: the words, then the words >> 8
 constexpr int kKsSlot = 1024;
 constexpr int kLdsKsDummy = kLdsKs + kSlots * kKsSlot;   // 1 KiB sink for the K-scale writes of threads 256..511
-constexpr int kLdsBytes = kLdsKsDummy + 1024;
+// per-32-key V scales (extension): kSlots x 512 B (4 blocks of 32 keys x 128 columns), then a 2 KiB sink for the
+// copies of the waves that carry none
+constexpr int kVsSlot = 512;
+constexpr int kLdsVs = kLdsKsDummy + 1024;
+constexpr int kLdsVsSink = kLdsVs + kSlots * kVsSlot;
+constexpr int kLdsBytes = kLdsVsSink + 2048;
 
 struct Prm {
     const uint8_t* q;
@@ -76,6 +81,10 @@ struct Prm {
     float* lse;
     uint32_t splits, rows_total;
     uint32_t f32_partials;   // kvsplit extension: partial rows as f32 (512 B) instead of fp16 (256 B)
+    // extension: per-32-key V scales; ptr_v_descale then holds E8M0 [B, ceil(SK/32), HK, 128] (vs_row = HK 128 bytes per
+    // 32-key block, vs_b = ceil(SK/32) vs_row per batch) and the per-tensor descale is 1
+    const uint8_t* vs32;
+    uint32_t vs_row, vs_b;
 #ifdef FMHA_TRACE
     uint64_t* trace;   // debug builds only: per (block, wave) timestamps, pointer at kernarg 0x288
     uint64_t t_entry;  // timestamp of the kernel's first instruction
@@ -137,6 +146,9 @@ __device__ inline Prm prm_from_kernarg() {
     p.k_b = KA_FIELD(uint32_t, s_k_Bs); p.v_seq = KA_FIELD(uint32_t, s_v_Seqs); p.v_b = KA_FIELD(uint32_t, s_v_Bs);
     p.o_seq = KA_FIELD(uint32_t, s_o_Seqs); p.o_b = KA_FIELD(uint32_t, s_o_Bs);
     p.qs_b = KA_FIELD(uint32_t, s_descale_q_Bs); p.ks_b = KA_FIELD(uint32_t, s_descale_k_Bs);
+    p.vs32 = (p.flags & FMHA_FLAG_V_SEQ32) ? (const uint8_t*)p.vd : nullptr;
+    p.vs_row = p.k_seq;
+    p.vs_b = ((p.SK + 31u) >> 5) * p.vs_row;
     p.ohat = nullptr; p.lse = nullptr; p.splits = 1; p.rows_total = 0; p.f32_partials = 0;
 #ifdef FMHA_TRACE
     p.trace = (uint64_t*)(uintptr_t)(ka<uint32_t>(0x288) | ((uint64_t)ka<uint32_t>(0x28C) << 32));
@@ -215,6 +227,14 @@ __device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uin
                  : "memory");
 }
 
+// The same with 4 bytes per lane: lane L's bytes land at lds_base + 4 L.
+__device__ inline void dma4(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory");
+}
+
 // Register-staged copy of one 128-key tile (K and V: 16 KiB each; K scales: 512 B) from HBM into an LDS ring
 // slot: load() issues the buffer loads into VGPRs, store() writes them (after the slot is free) with ds_write_b128.
 // Thread tid moves 16-byte chunk (tid & 7) of rows i NT/8 + tid/8, i < kN: each 8-thread group reads one
@@ -236,6 +256,36 @@ struct Stager {
     uint32_t ksshift;   // 0 for the words (tid < 128), 8 for the shifted copies (128 <= tid < 256)
     uint32_t woff;      // (tid / 8) 128 + 16 ((tid & 7) ^ swz(tid / 8))
     uint32_t tid, k_seq, ks_row, SK, lds;
+    const uint8_t* vsb; // per-32-key V scales of this (batch, KV head) (extension; unused otherwise)
+    uint32_t vs_row;    // bytes between consecutive 32-key blocks of the V-scale tensor (HK 128)
+
+    __device__ void init_vs(const uint8_t* vsb_, uint32_t vs_row_) {
+        vsb = uniform_ptr(vsb_);
+        vs_row = vs_row_;
+    }
+    // Resource over the V-scale rows of blocks [blk0, ceil(SK/32)) of this head (empty when `valid` is false or blk0 is
+    // past the last block, so such lanes read zeros: E8M0 0, a finite scale for the zero V rows past SK)
+    __device__ __forceinline__ __amdgpu_buffer_rsrc_t vs_rsrc(uint32_t blk0, bool valid) const {
+        const uint32_t nb = (SK + 31u) >> 5;
+        const bool live = valid && blk0 < nb;
+        const uint32_t bytes = live ? (nb - 1u - blk0) * vs_row + 128u : 0u;
+        return make_rsrc(vsb + (size_t)(live ? blk0 : 0u) * vs_row, bytes);
+    }
+    // Direct copy of tile [key0, key0 + 128)'s V scales (4 blocks x 128 columns) into V-scale slot `slot`: waves 0 and 1
+    // copy two blocks each (lane L: block 2w + L / 32, columns 4 (L % 32) ..); the other waves copy from an empty
+    // resource into the sink, so that every wave issues exactly one copy per phase.
+    __device__ __forceinline__ void dma_vs(uint32_t key0, bool valid, uint32_t slot) const {
+        const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63u;
+        const uint32_t dst = w < 2u ? slot_base(lds, kLdsVs, slot, kVsSlot) + 256u * w : lds + kLdsVsSink + 256u * (w - 2u);
+        dma4(vs_rsrc((key0 >> 5) + 2u * w, valid && w < 2u), dst, (lane >> 5) * vs_row + 4u * (lane & 31u), 0u);
+    }
+    // Register-staged variant (threads 0..127: one word each, block tid / 32, columns 4 (tid % 32) ..)
+    __device__ __forceinline__ uint32_t load_vs(uint32_t key0, bool valid) const {
+        return __builtin_amdgcn_raw_buffer_load_b32(vs_rsrc(key0 >> 5, valid && tid < 128u), (tid >> 5) * vs_row + 4u * (tid & 31u), 0, 0);
+    }
+    __device__ __forceinline__ void store_vs(uint32_t word, uint32_t slot) const {
+        if (tid < 128u) lds_write4(slot_base(lds, kLdsVs, slot, kVsSlot) + 4u * tid, word);
+    }
 
     __device__ void init(const uint8_t* kb_, const uint8_t* vb_, const uint8_t* ksb_, uint32_t k_seq_, uint32_t SK_, uint32_t lds_) {
         // wave-uniform base pointers (readfirstlane states it), so the per-tile resource arithmetic stays scalar
@@ -448,6 +498,7 @@ struct Wave {
     uint32_t vfo;      // V^T read offset: row rlo, chunk ((g & 1) ^ swz(rlo)), half pp; dim group dc = vfo ^ (2 dc) << 4
     uint32_t onew;
     uint32_t kso;      // K-scale word offset of this lane: hh 512 + 4 n
+    uint32_t vso;      // V-scale byte offset of this lane in a slot: block hh of the 64-key half, column n (+ 32 dc)
     // causal limits: query row i sees keys [0, i + SK - S + 1) (cut to [.., key_hi))
     uint32_t lim_row, lim_wave_min, lim_wave_max, key_hi;
     // softmax state
@@ -479,6 +530,7 @@ struct Wave {
         const uint32_t row_c = min(row, p.S - 1u);
         kfo = n * 128u + ((hh ^ swz(n)) << 4);
         kso = hh * 512u + n * 4u;
+        vso = hh * 128u + n;
         {
             const uint8_t* qrow = p.q + (size_t)bidx * p.q_b + (size_t)row_c * p.q_seq + head * kD;
 #pragma unroll
@@ -487,7 +539,7 @@ struct Wave {
                 for (int e = 0; e < 2; ++e) qtmp[2 * c + e] = *(const GLOBAL_AS v4i*)(qrow + 64 * c + 32 * e + 16 * hh);
         }
         qsw = *(const GLOBAL_AS uint32_t*)(p.qs + (size_t)bidx * p.qs_b + (size_t)row_c * (p.H * 4u) + head * 4u);
-        vd = *(const GLOBAL_AS float*)p.vd;
+        vd = p.vs32 ? 1.0f : *(const GLOBAL_AS float*)p.vd;   // per-32-key V scales ride in the PV MFMAs instead
         lim_row = lim_wave_min = lim_wave_max = key_hi;
         if (p.flags & 1u) {
             const int off = (int)p.SK - (int)p.S + 1;
@@ -538,6 +590,11 @@ struct Wave {
     // K-scale word of 32-key block t4 for this lane's key row, read from the copy shifted down by hh bytes so that
     // op_sel byte 2c is the lane half's E8M0 byte 2c + hh
     __device__ __forceinline__ uint32_t kscale(uint32_t ksb, int t4) const { return lds_read4(lane_addr(ksb, kso) + 128u * t4); }
+    // E8M0 of PV MFMA (j, dc)'s k-block for this lane: in the scaled MFMA, lane r + 32 kb supplies the scale of row r
+    // (column 32 dc + n) over k-block kb, which is 32-key block 2 j + kb of the tile (the S^T tile the P bytes came from)
+    __device__ __forceinline__ uint32_t vscale(uint32_t vsb, int j, int dc) const {
+        return *(const LDS_AS uint8_t*)(uintptr_t)(lane_addr(vsb, vso) + 256u * j + 32u * dc);
+    }
     // V^T fragment of PV MFMA (j, dc): four transposing reads 16 keys apart
     __device__ __forceinline__ v8i vfrag(uint32_t vb, int j, int dc) const {
         const uint32_t va = lane_addr(vb, vfo ^ ((uint32_t)(2 * dc) << 4)) + 8192u * j;
@@ -563,8 +620,15 @@ struct Wave {
 
     // PV of one tile: O^T += V^T P^T (8 MFMAs) and the row sums of P (2 MFMAs). Each V^T fragment is read one MFMA
     // ahead; a scheduling fence after every MFMA keeps the compiler from hoisting the phase's 32 reads to its top.
+    template <bool VS = false>
     __device__ __forceinline__ void pv_all(uint32_t slot, const uint32_t (&pw)[4][4]) {
         const uint32_t vb = slot_base(lds, kLdsV, slot, kTileBytes);
+        uint32_t vsc[8];
+        if (VS) {
+            const uint32_t vsb = slot_base(lds, kLdsVs, slot, kVsSlot);
+#pragma unroll
+            for (int g = 0; g < 8; ++g) vsc[g] = vscale(vsb, g >> 2, g & 3);
+        }
         v8i vf = vfrag(vb, 0, 0);
 #pragma unroll
         for (int g = 0; g < 8; ++g) {
@@ -573,7 +637,7 @@ struct Wave {
             v8i vn = vf;
             if (g < 7) vn = vfrag(vb, (g + 1) >> 2, (g + 1) & 3);
             if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones_op(), pf, lacc, 0, 0, 0, 127, 0, 127);
-            o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, o[dc], 0, 0, 0, 127, 0, 127);
+            o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, o[dc], 0, 0, 0, VS ? (int)vsc[g] : 127, 0, 127);
             vf = vn;
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -628,10 +692,16 @@ struct Wave {
         for (int t4 = 0; t4 < 4; ++t4) pre.ksw[t4] = kscale(ksb, t4);
     }
 
-    template <bool QK>
+    template <bool QK, bool VS = false>
     __device__ __forceinline__ float m_phase_qf(uint32_t vslot, const uint32_t (&pw)[4][4], uint32_t kslot, v16f (&s)[4], Ring& ring,
                                                 const QkPre& pre) {
         const uint32_t vb = slot_base(lds, kLdsV, vslot, kTileBytes);
+        uint32_t vsc[8];   // per-32-key V scales of the 8 PV MFMAs (extension), read a few MFMAs ahead of PV
+        auto read_vs = [&] {
+            const uint32_t vsb = slot_base(lds, kLdsVs, vslot, kVsSlot);
+#pragma unroll
+            for (int g = 0; g < 8; ++g) vsc[g] = vscale(vsb, g >> 2, g & 3);
+        };
         const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
         constexpr int I0 = QK ? 0 : 8;
         auto fetch = [&](int i) -> v8i {
@@ -644,12 +714,14 @@ struct Wave {
 #pragma unroll
             for (int i = I0; i < I0 + DEPTH; ++i) ring[i % (DEPTH + 1)] = fetch(i);
             ones = ones_op();
+            if (VS) read_vs();
         }
 #pragma unroll
         for (int i = I0; i < 16; ++i) {
             if (i + DEPTH < 16) ring[(i + DEPTH) % (DEPTH + 1)] = fetch(i + DEPTH);
             if (QK && i == 2) qf1 = qfrag(1);
             if (QK && i == 5) ones = ones_op();
+            if (VS && QK && i == 4) read_vs();
             __builtin_amdgcn_sched_barrier(0);
             if (i < 8) {
                 const int c = i >> 2, t4 = i & 3;
@@ -658,7 +730,8 @@ struct Wave {
                 const int j = (i - 8) >> 2, dc = (i - 8) & 3;
                 const v8i pf = pfrag(pw, j);
                 if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, pf, lacc, 0, 0, 0, 127, 0, 127);
-                o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ring[i % (DEPTH + 1)], pf, o[dc], 0, 0, 0, 127, 0, 127);
+                o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ring[i % (DEPTH + 1)], pf, o[dc], 0, 0, 0,
+                                                                         VS ? (int)vsc[i - 8] : 127, 0, 127);
             }
             __builtin_amdgcn_sched_barrier(0);
             // row max of S(t+1): accumulator (i - 9) behind PV MFMAs 9..12 (accumulator a's last QK MFMA is i = 4 + a)
@@ -764,7 +837,7 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
 // B M(t-1); f = 2t + 1: A M(t), B V(t). Tile u's slot (u % 3) is read in phases 2u-1 .. 2u+2 and must be written
 // before 2u-1: A writes its share of tile t+1 in V(t) (loaded in M(t-1)), B its share of tile t+2 in V(t)
 // (loaded in M(t-1)); every write lands in a slot whose last read phase has passed.
-template <bool LUT, bool SPLIT, bool GB>
+template <bool LUT, bool SPLIT, bool GB, bool VS>
 __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx,
                                                       uint32_t split, uint32_t key_lo, uint32_t key_hi) {
     constexpr int NT = 512;
@@ -787,6 +860,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     Stager<NT> st;
     st.init(p.k + (size_t)bidx * p.k_b + kvh * kD, p.v + (size_t)bidx * p.v_b + kvh * kD, p.ks + (size_t)bidx * p.ks_b + kvh * 4u,
             p.k_seq, p.SK, lds);
+    if (VS) st.init_vs(p.vs32 + (size_t)bidx * p.vs_b + kvh * kD, p.vs_row);
     auto slot_of = [](uint32_t t) { return t % 3u; };
     auto key_of = [&](uint32_t t) { return key_lo + t * kTile; };
 
@@ -803,10 +877,11 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
         // K/V tiles go HBM -> LDS by direct copies. V(t) issues K tile t+2 and V tile t+1 into the slots the register-
         // staged path writes in V(t), with the K-scale words (register-staged, loaded one phase ahead); the barrier that
         // ends V(t+1) (A) or M(t+1) (B) waits for them (vmcnt counts in issue order: this phase's copies stay in flight).
-        constexpr int kDmaOps = 2 * Stager<NT>::kN + 1;   // VMEM operations issued per VALU phase
+        constexpr int kDmaOps = 2 * Stager<NT>::kN + 1 + (VS ? 1 : 0);   // VMEM operations issued per VALU phase
         st.init_dma();
         st.dma(key_of(0), true, 0, key_of(0), true, 0);                 // K 0, V 0
         st.dma(key_of(1), ntiles > 1, 1, key_of(1), false, 2);          // K 1
+        if (VS) st.dma_vs(key_of(0), true, 0);                          // V scales of tile 0
         st.load_ks(key_of(0), true);
         st.store_ks(0);
         st.load_ks(key_of(1), ntiles > 1);
@@ -826,6 +901,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
                 FMHA_SETPRIO(0);
                 st.store_ks(slot_of(t + 2));
                 st.dma(key_of(t + 2), t + 2 < ntiles, slot_of(t + 2), key_of(t + 1), t + 1 < ntiles, slot_of(t + 1));
+                if (VS) st.dma_vs(key_of(t + 1), t + 1 < ntiles, slot_of(t + 1));
                 st.load_ks(key_of(t + 3), t + 3 < ntiles);
                 if (w.needs_mask(key_of(t))) {
                     w.apply_mask(s, key_of(t));
@@ -849,7 +925,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
             for (; t + 1 < ntiles; ++t) {
                 uint32_t pw[4][4];
                 v_phase(t, pw, false);
-                mrow = w.template m_phase_qf<true>(slot_of(t), pw, slot_of(t + 1), s, ring, pre);
+                mrow = w.template m_phase_qf<true, VS>(slot_of(t), pw, slot_of(t + 1), s, ring, pre);
                 FMHA_LMARK(p, tblk, t, 2);
                 if (GB) block_barrier_keep_dma<0, kDmaOps>();
                 else asm volatile("" ::: "memory");   // A: the compiler-only fence where B has its barrier
@@ -859,7 +935,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
                 // the last tile: PV only
                 uint32_t pw[4][4];
                 v_phase(t, pw, true);
-                (void)w.template m_phase_qf<false>(slot_of(t), pw, slot_of(t), s, ring, pre);
+                (void)w.template m_phase_qf<false, VS>(slot_of(t), pw, slot_of(t), s, ring, pre);
                 if (GB) block_barrier();
             }
         }
@@ -874,18 +950,18 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
 
 // The whole routine is instantiated per group (the groups place their barrier differently; one body with a
 // group-dependent branch, or two loop copies sharing a prologue, made the register allocation spill).
-template <bool LUT, bool SPLIT>
+template <bool LUT, bool SPLIT, bool VS>
 __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split,
                                 uint32_t key_lo, uint32_t key_hi) {
-    if (wave_id() >= 4u) attend_pingpong_group<LUT, SPLIT, true>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
-    else attend_pingpong_group<LUT, SPLIT, false>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
+    if (wave_id() >= 4u) attend_pingpong_group<LUT, SPLIT, true, VS>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
+    else attend_pingpong_group<LUT, SPLIT, false, VS>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
 }
 
 // One 4-wave group (_t128: one wave per SIMD, so each wave overlaps its own VALU with its own MFMAs): S(t) is
 // computed and decided one iteration ahead. Iteration t: [P(t) conversion | QK(t+1)] then [PV(t) | row max of
 // S(t+1)]; the tile t+2 staged through registers lands in slot (t+2) % 3 (tile t-1's: its last read was in
 // iteration t-1), one barrier, then the rebase decision of tile t+1. The last tile runs [P | PV] alone.
-template <bool LUT, int NT = 256>
+template <bool LUT, bool VS, int NT = 256>
 __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_lo,
                                  uint32_t key_hi) {
     const Recipe rc = recipe(LUT);
@@ -899,16 +975,24 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
     Stager<NT> st;
     st.init(p.k + (size_t)bidx * p.k_b + kvh * kD, p.v + (size_t)bidx * p.v_b + kvh * kD, p.ks + (size_t)bidx * p.ks_b + kvh * 4u,
             p.k_seq, p.SK, lds);
+    if (VS) st.init_vs(p.vs32 + (size_t)bidx * p.vs_b + kvh * kD, p.vs_row);
     auto key_of = [&](uint32_t t) { return key_lo + t * kTile; };
 
     v16f s[4];
     if (ntiles > 0) {
         typename Stager<NT>::Regs r0;
         st.load_into(r0, key_of(0), true, key_of(0), true);
+        uint32_t vs0 = 0, vs1 = 0;   // V-scale words of tiles 0 and 1 (extension)
+        if (VS) vs0 = st.load_vs(key_of(0), true);
         st.load(key_of(1), ntiles > 1, key_of(1), ntiles > 1);
+        if (VS) vs1 = st.load_vs(key_of(1), ntiles > 1);
         w.commit_q();
         st.store_from(r0, 0, 0);
         if (ntiles > 1) st.store(1, 1);
+        if (VS) {
+            st.store_vs(vs0, 0);
+            st.store_vs(vs1, 1);
+        }
         block_barrier();
         if (w.active(key_of(0))) {
             w.qk_all(0, s);
@@ -920,6 +1004,8 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
             const uint32_t nslot = slot == 2u ? 0u : slot + 1u;
             const uint32_t sslot = nslot == 2u ? 0u : nslot + 1u;   // slot of tile t+2
             st.load(key_of(t + 2), t + 2 < ntiles, key_of(t + 2), t + 2 < ntiles);
+            uint32_t vs2 = 0;
+            if (VS) vs2 = st.load_vs(key_of(t + 2), t + 2 < ntiles);
             const bool act = w.active(key_of(t)), act_next = w.active(key_of(t + 1));
             uint32_t pw[4][4];
             if (act_next) {
@@ -942,13 +1028,14 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
 #pragma unroll
                 for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
             }
-            if (act) w.pv_all(slot, pw);
+            if (act) w.template pv_all<VS>(slot, pw);
             float m = 0.0f;
             if (act_next) {
                 if (w.needs_mask(key_of(t + 1))) w.apply_mask(s, key_of(t + 1));
                 m = row_max(s);
             }
             if (t + 2 < ntiles) st.store(sslot, sslot);
+            if (VS && t + 2 < ntiles) st.store_vs(vs2, sslot);
             block_barrier();
             if (act_next) rebase<LUT>(rc, m, s, w.o, w.lacc, w.bias, w.bw);
             slot = nslot;
@@ -957,7 +1044,7 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
             uint32_t pw[4][4];
 #pragma unroll
             for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
-            w.pv_all(slot, pw);
+            w.template pv_all<VS>(slot, pw);
         }
     }
     epilogue<false>(p, w, head, bidx, 0, rc);
@@ -992,11 +1079,21 @@ __device__ void full_kernel(uint32_t lds) {
     block_coords(p.S, p.H, NT / 2, qt, head, z);
     const bool lut = (p.SK + 127u) / 128u < 4u;   // state.rs:75-77
     if (NT == 512) {
-        if (lut) attend_pingpong<true, false>(p, lds, qt, head, z, 0, 0, p.SK);
-        else attend_pingpong<false, false>(p, lds, qt, head, z, 0, 0, p.SK);
+        if (p.vs32) {
+            if (lut) attend_pingpong<true, false, true>(p, lds, qt, head, z, 0, 0, p.SK);
+            else attend_pingpong<false, false, true>(p, lds, qt, head, z, 0, 0, p.SK);
+        } else {
+            if (lut) attend_pingpong<true, false, false>(p, lds, qt, head, z, 0, 0, p.SK);
+            else attend_pingpong<false, false, false>(p, lds, qt, head, z, 0, 0, p.SK);
+        }
     } else {
-        if (lut) attend_pipelined<true>(p, lds, qt, head, z, 0, p.SK);
-        else attend_pipelined<false>(p, lds, qt, head, z, 0, p.SK);
+        if (p.vs32) {
+            if (lut) attend_pipelined<true, true>(p, lds, qt, head, z, 0, p.SK);
+            else attend_pipelined<false, true>(p, lds, qt, head, z, 0, p.SK);
+        } else {
+            if (lut) attend_pipelined<true, false>(p, lds, qt, head, z, 0, p.SK);
+            else attend_pipelined<false, false>(p, lds, qt, head, z, 0, p.SK);
+        }
     }
 }
 
@@ -1029,6 +1126,7 @@ extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvs
     const uint32_t split_field = ka<uint32_t>(offsetof(fmha_mxfp8_kvsplit_args, kvs_splits));
     p.splits = split_field & 0xffffu;
     p.f32_partials = (split_field & FMHA_KVS_F32_PARTIALS) ? 1u : 0u;
+    p.vs32 = (split_field & FMHA_KVS_V_SEQ32) ? (const uint8_t*)p.vd : nullptr;   // 0x280 is not `flags` here
     p.rows_total = ka<uint32_t>(offsetof(fmha_mxfp8_kvsplit_args, kvs_rows_total));
     uint32_t qt, head, z;
     block_coords(p.S, p.H, 256u, qt, head, z);
@@ -1040,8 +1138,13 @@ extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvs
     const uint32_t tile_hi = min(ntiles, tile_lo + tps);
     const uint32_t key_lo = tile_lo * 128u, key_hi = min(tile_hi * 128u, p.SK);
     const bool lut = ntiles < 4u;
-    if (lut) attend_pingpong<true, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
-    else attend_pingpong<false, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+    if (p.vs32) {
+        if (lut) attend_pingpong<true, true, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+        else attend_pingpong<false, true, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+    } else {
+        if (lut) attend_pingpong<true, true, false>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+        else attend_pingpong<false, true, false>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+    }
 }
 
 // epilogue.rs:89-167 / io.rs:164-185: thread t -> 8 consecutive outputs of row t >> 4 (tail threads redo the last group)

@@ -59,7 +59,8 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     q        [B, S, H, 128]   fp8 e4m3 (uint8 or float8_e4m3fn)   k, v [B, SK, HK, 128] (H = gqa HK, gqa a power of two <= 16)
     q_scale  [B, S, H, 4]     E8M0 bytes          k_scale [B, SK, HK, 4]; both need the zeroed slack tail of the
                                                    kernel contract (512 H 4 / 640 H 4 bytes behind the tensor)
-    v_scale  f32 V descale in a buffer of at least 4096 bytes
+    v_scale  f32 V descale in a buffer of at least 4096 bytes, or (extension) a uint8 E8M0 tensor
+             [B, ceil(SK/32), HK, 128]: one scale per 32 keys per column (``quantize_v_seq32``'s output)
     out      [B, S, H, 128]   bf16
     path: "auto" | "vs128" | "t128" | "kvsplit" (``splits`` in {2, 4, 8}). Returns (path, splits).
     Extensions (not in the reference): ``lse`` [B, H, S] f32 receives the natural-log LSE (vs128 / t128);
@@ -78,7 +79,10 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     _expect(q_scale, "q_scale", (B, S, H, 4), 1, align=4)
     _expect(k_scale, "k_scale", (B, SK, HK, 4), 1, align=4)
     _expect(out, "out", (B, S, H, D), 2)
-    if _cap(v_scale) < 4:
+    v_seq32 = v_scale.dtype == torch.uint8 and v_scale.dim() == 4
+    if v_seq32:
+        _expect(v_scale, "v_scale", (B, (SK + 31) // 32, HK, D), 1)
+    elif _cap(v_scale) < 4:
         raise ValueError("v_scale: needs at least one f32")
     if lse is not None:
         _expect(lse, "lse", (B, H, S), 4)
@@ -103,6 +107,7 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     p.B, p.H, p.HK, p.S, p.SK = B, H, HK, S, SK
     p.path, p.splits, p.causal = path_id, nsplit, int(bool(causal))
     p.f32_partials = int(partials == "fp32")
+    p.v_seq32 = int(v_seq32)
     # the workspace only matters for the KV split; size it for the split the dispatch will choose
     want_path, want_splits = (select_path(B, H, S, SK) if path_id < 0 else (path, nsplit))
     ws, ws_bytes = None, 0
@@ -181,11 +186,13 @@ def quantize_v_seq32(x, stream=None):
 LOG2E_OVER_SQRT_D = 1.4426950408889634 / math.sqrt(D)
 
 
-def fmha_fwd_bf16_via_mxfp8(q, k, v, out=None, *, softmax_scale=None, causal=False, path="auto", splits=None, lse=None, stream=None):
+def fmha_fwd_bf16_via_mxfp8(q, k, v, out=None, *, softmax_scale=None, causal=False, path="auto", splits=None, lse=None, stream=None,
+                            v_scales="tensor"):
     """Attention from bf16 q [B, S, H, 128], k / v [B, SK, HK, 128]: quantises on the GPU (Q scaled by
     softmax_scale * log2(e) before quantisation, default 1/sqrt(128), as ref_host.cpp:238 folds it), then runs
     ``fmha_fwd_mxfp8``. Returns out (bf16 [B, S, H, 128]); ``lse``, when given, receives the natural-log LSE of
-    the scaled scores."""
+    the scaled scores. ``v_scales``: "tensor" (one f32 descale, the reference's) or "seq32" (extension: one E8M0 per
+    32 keys per column)."""
     B, S, H, _ = q.shape
     _, SK, HK, _ = k.shape
     mul = LOG2E_OVER_SQRT_D if softmax_scale is None else 1.4426950408889634 * float(softmax_scale)
@@ -193,7 +200,12 @@ def fmha_fwd_bf16_via_mxfp8(q, k, v, out=None, *, softmax_scale=None, causal=Fal
     ks = alloc_scales(B, SK, HK, k.device)
     q8 = quantize_mxfp8(q, qs, mul=mul, stream=stream)
     k8 = quantize_mxfp8(k, ks, stream=stream)
-    v8, vs = quantize_v(v, stream=stream)
+    if v_scales == "seq32":
+        v8, vs = quantize_v_seq32(v, stream=stream)
+    elif v_scales == "tensor":
+        v8, vs = quantize_v(v, stream=stream)
+    else:
+        raise ValueError(f"v_scales must be 'tensor' or 'seq32', got {v_scales!r}")
     if out is None:
         out = torch.empty(B, S, H, D, dtype=torch.bfloat16, device=q.device)
     fmha_fwd_mxfp8(q8, k8, v8, qs, ks, vs, out, path=path, splits=splits, stream=stream, lse=lse, causal=causal)

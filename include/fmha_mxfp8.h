@@ -99,7 +99,7 @@ typedef struct fmha_mxfp8_args {
     uint8_t _pad25[12];
     uint32_t s_descale_k_Hs;  /* 0x260 4 */
     uint8_t _pad26[28];
-    uint32_t flags;           /* 0x280 extension flags, 0 = reference semantics; bit 0 = bottom-right causal mask */
+    uint32_t flags;           /* 0x280 extension flags, 0 = reference semantics: FMHA_FLAG_CAUSAL, FMHA_FLAG_V_SEQ32 */
     uint8_t abi_tail[12];     /* 0x284 */
 } fmha_mxfp8_args;
 
@@ -133,6 +133,15 @@ typedef struct fmha_mxfp8_combine_args {
  * filling the fp32-sized rows the workspace already has) and the combine read them so. The split count is the low
  * 16 bits of either field; a launcher that follows the reference never sets bit 16. */
 #define FMHA_KVS_F32_PARTIALS 0x10000u
+
+/* Extensions of the full-sequence kernels' `flags` (0x280), no counterpart in the reference's MX kernels:
+ *   FMHA_FLAG_CAUSAL    the bottom-right causal mask: key t visible to query i iff t <= i + SK - S;
+ *   FMHA_FLAG_V_SEQ32   per-32-key V scales: ptr_v_descale (0x220) points to E8M0 bytes [B, ceil(SK/32), HK, 128]
+ *                       (one per 32 keys per column, the layout of fmha_mxfp8_quantize_seq32) instead of one f32.
+ * For the KV split, FMHA_KVS_V_SEQ32 is OR-ed into kvs_splits (0x280) with the same meaning. */
+#define FMHA_FLAG_CAUSAL 0x1u
+#define FMHA_FLAG_V_SEQ32 0x2u
+#define FMHA_KVS_V_SEQ32 0x20000u
 
 /* Byte sizes of the caller's allocations, checked by the validate calls
  * (the reference's BufferSizes, ..._vs128_abi.h:131-139). */
@@ -220,6 +229,7 @@ typedef struct fmha_mxfp8_params {
     int32_t splits;            /* KV split count when path == FMHA_PATH_KVSPLIT (2, 4 or 8; 0 = 4) */
     int32_t causal;            /* 0 = the reference semantics; 1 = bottom-right causal mask (extension) */
     int32_t f32_partials;      /* KV split only: 0 = fp16 partial rows (the reference's); 1 = f32 (extension) */
+    int32_t v_seq32;           /* 0 = v_descale is one f32 (the reference's); 1 = E8M0 per 32 keys per column (extension) */
 } fmha_mxfp8_params;
 
 /* fmha_fwd_hd128_mxfp8_auto: dispatch + validate + launch (+ combine), all on

@@ -19,7 +19,10 @@ def upload(inp, device):
     ks_all = t(inp.ks)
     qs = qs_all[: B * S * H * 4].view(B, S, H, 4)
     ks = ks_all[: B * SK * HK * 4].view(B, SK, HK, 4)
-    vs = t(inp.vd_buf)
+    if inp.vs32 is not None:   # extension: per-32-key V scales [B, ceil(SK/32), HK, 128]
+        vs = t(inp.vs32).view(B, (SK + 31) // 32, HK, D)
+    else:
+        vs = t(inp.vd_buf)
     return q, k, v, qs, ks, vs
 
 

@@ -156,7 +156,7 @@ def test_validate_f32_partials_flag():
     ka, sz, g = _kvsplit()
     ka.kvs_splits = 8 | lib.KVS_F32_PARTIALS
     assert lib.validate("kvsplit", ka, sz, g, B=1, HK=8, KL=0) == (0, "")
-    ka.kvs_splits = 8 | (1 << 17)
+    ka.kvs_splits = 8 | (1 << 18)
     rc, msg = lib.validate("kvsplit", ka, sz, g, B=1, HK=8)
     assert rc == lib.FMHA_ERR_KA_RANGE and "0x280" in msg
     ca = lib.CombineArgs(0x1, 0x2, 0x3, 1024, 128, 8 | lib.KVS_F32_PARTIALS)
@@ -164,6 +164,32 @@ def test_validate_f32_partials_flag():
     assert lib.validate("combine", ca, csz, (64, 1, 1)) == (0, "")
     ca.splits = 8 | (1 << 20)
     assert lib.validate("combine", ca, csz, (64, 1, 1))[0] == lib.FMHA_ERR_KA_RANGE
+
+
+def test_validate_v_seq32_flag():
+    """Per-32-key V scales (extension, flags bit 1 / kvs_splits bit 17): ptr_v_descale must then hold the E8M0 tensor
+    [B, ceil(SK/32), HK, 128] instead of 4 KiB; unknown flag bits are out of contract."""
+    B, H, HK, S, SK = 2, 8, 4, 300, 1000
+    a, sz = _shape_args(B, H, HK, S, SK)
+    grid = (math.ceil(S / 256), H, B)
+    need = B * math.ceil(SK / 32) * HK * 128
+    a.flags = lib.FLAG_V_SEQ32
+    sz.ptr_v_descale = need
+    assert lib.validate("vs128", a, sz, grid, HK=HK) == (0, "")
+    sz.ptr_v_descale = need - 1
+    assert lib.validate("vs128", a, sz, grid, HK=HK)[0] == lib.FMHA_ERR_EXTENT
+    sz.ptr_v_descale = need
+    a.flags = lib.FLAG_V_SEQ32 | lib.FLAG_CAUSAL
+    assert lib.validate("vs128", a, sz, grid, HK=HK) == (0, "")
+    a.flags = 0x4
+    rc, msg = lib.validate("vs128", a, sz, grid, HK=HK)
+    assert rc == lib.FMHA_ERR_KA_RANGE and "0x280" in msg
+    ka, ksz, g = _kvsplit(B=1, H=8, HK=8, S=128, SK=16384, splits=8)
+    ka.kvs_splits = 8 | lib.KVS_V_SEQ32
+    ksz.ptr_v_descale = 4096
+    assert lib.validate("kvsplit", ka, ksz, g, B=1, HK=8)[0] == lib.FMHA_ERR_EXTENT
+    ksz.ptr_v_descale = 16384 // 32 * 8 * 128
+    assert lib.validate("kvsplit", ka, ksz, g, B=1, HK=8, KL=0) == (0, "")
 
 
 def test_validate_combine():

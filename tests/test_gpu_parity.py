@@ -129,6 +129,39 @@ def test_parity_f32_partials(gpu, case):
     assert cmp["max_abs"] <= 0.05, cmp
 
 
+# Extension: per-32-key V scales (V re-quantised with one E8M0 per 32 keys per column; the PV MFMAs apply them).
+# Bar: the statistical one against the oracle's emulation of the same inputs, and element-wise closeness to it.
+VS32_CASES = [
+    ("vs128_B2H8S1024", 2, 8, 8, 1024, 1024, False, "vs128", None),
+    ("vs128_ragged_B1H8HK2_S700_SK1000", 1, 8, 2, 700, 1000, False, "vs128", None),   # SK % 32 != 0, GQA 4
+    ("t128_B1H4S512_SK600", 1, 4, 4, 512, 600, False, "t128", None),
+    ("t128_short_SK100", 1, 2, 2, 256, 100, False, "t128", None),                     # < 4 tiles: the LUT recipe
+    ("kvsplit_B1H8S128_SK4000_split4", 1, 8, 8, 128, 4000, False, "kvsplit", 4),
+    ("causal_vs128_B1H8S1024", 1, 8, 8, 1024, 1024, True, "vs128", None),
+]
+
+
+@pytest.mark.parametrize("case", VS32_CASES, ids=[c[0] for c in VS32_CASES])
+def test_parity_v_seq32(gpu, case):
+    name, B, H, HK, S, SK, causal, path, splits = case
+    print(f"[case] v_seq32 {name}", flush=True)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal, v_seq32=True)
+    out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
+    assert used[0] == path
+    used_splits = used[1] if used[0] == "kvsplit" else 0
+    rows = min(S, 256 if causal else ROWS)
+    emu = oracle.emulate(inp, splits=used_splits, rows=rows)
+    ref_stats = oracle.check_fp64(inp, emu, rows=rows)
+    stats = oracle.check_fp64(inp, out, rows=rows)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
+    print(f"[case] v_seq32 {name} path={used} ours={stats} emulated={ref_stats} vs-emulation={cmp}", flush=True)
+    assert not np.isnan(oracle.bf16_to_f32(out)).any()
+    assert stats["bad"] <= ref_stats["bad"]
+    assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"]
+    assert cmp["mean_abs"] <= 0.6 * ref_stats["mean_err"], cmp
+    assert cmp["max_abs"] <= 0.05, cmp
+
+
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("shape", [(1, 4, 4, 512, 640), (4, 8, 8, 1024, 1024)], ids=["t128", "vs128"])
 def test_lse_output(gpu, shape, causal):
