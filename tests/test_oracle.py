@@ -385,8 +385,8 @@ def test_emulated_f32_partials():
 
 def test_emulation_v_seq32_scales():
     """Per-32-key V scales (extension) in the recipe emulation: raising every scale by one binade doubles the output
-    exactly; raising only block 1 of column 5 changes only column 5, and only for rows that see keys 32..63; the
-    statistics stay those of the per-tensor V (same data, re-quantised)."""
+    exactly; raising only block 1 of column 5 changes only column 5; the statistics stay those of the per-tensor V (same
+    data, re-quantised)."""
     inp = oracle.Inputs(1, 2, 48, 100, v_seq32=True)
     base = oracle.bf16_to_f32(oracle.emulate(inp, rows=0)).reshape(1, 48, 2, D)
     keep = inp.vs32.copy()
