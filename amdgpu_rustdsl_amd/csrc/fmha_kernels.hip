@@ -53,7 +53,7 @@ namespace {
 constexpr int kD = 128;
 constexpr int kTile = 128;                    // keys per KV tile
 constexpr int kTileBytes = kTile * kD;        // 16 KiB
-constexpr int kSlots = 3;                     // ring depth (prefetch distance 2)
+constexpr int kSlots = 4;                     // ring depth of the direct-copy path (t128 uses 3 of the slots)
 constexpr int kLdsK = 0;                      // kSlots K tiles
 constexpr int kLdsV = kSlots * kTileBytes;    // kSlots V tiles
 constexpr int kLdsKs = 2 * kSlots * kTileBytes;   // kSlots x 1 KiB of K scales: the words, then the words >> 8
@@ -416,10 +416,11 @@ __device__ inline Recipe recipe(bool lut) {
 
 // Row max of one tile's S^T accumulators: the lane's 64 values (v_max3 chain), then the partner lane l ^ 32
 // (the other key half of the same query column) through v_permlane32_swap.
-__device__ __forceinline__ float row_max(const v16f (&s)[4]) {
+template <int NA>
+__device__ __forceinline__ float row_max(const v16f (&s)[NA]) {
     float m = -1.0e30f;
 #pragma unroll
-    for (int t4 = 0; t4 < 4; ++t4)
+    for (int t4 = 0; t4 < NA; ++t4)
 #pragma unroll
         for (int i = 0; i < 16; ++i) m = fmaxf(m, s[t4][i]);
     const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m), false, false);
@@ -428,8 +429,8 @@ __device__ __forceinline__ float row_max(const v16f (&s)[4]) {
 
 // The rebase decision of one tile given its row max m: when any lane's max passes the threshold, the new two-word
 // reference and the rescale of S, O and the row sums (lanes below the threshold keep their reference, delta = 0).
-template <bool LUT>
-__device__ __forceinline__ void rebase(const Recipe& rc, float m, v16f (&s)[4], v16f (&o)[4], v4f& lacc, float& bias, uint32_t& bw) {
+template <bool LUT, int NA>
+__device__ __forceinline__ void rebase(const Recipe& rc, float m, v16f (&s)[NA], v16f (&o)[4], v4f& lacc, float& bias, uint32_t& bw) {
     // softmax.rs:125-160 eager: thr < m; softmax.rs:186-241 lazy: !(thr >= m), which also takes NaN
     const bool grow = LUT ? (rc.thr < m) : !(rc.thr >= m);
     if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -447,7 +448,7 @@ __device__ __forceinline__ void rebase(const Recipe& rc, float m, v16f (&s)[4], 
         const float delta = grow ? b_q - b_old : 0.0f;
         bw = grow ? (h_raw | (l_raw << 16)) : bw;
 #pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4)
+        for (int t4 = 0; t4 < NA; ++t4)
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[t4][i] += delta;
         const float corr = __builtin_amdgcn_exp2f(delta * 512.0f);
@@ -518,14 +519,16 @@ struct Wave {
 
     // Lane constants, softmax state, and the loads of the lane's Q bytes and scales. The Q bytes stay in registers
     // (16 VGPRs) for the whole key range: re-reading them from LDS every tile cost 32 KiB of LDS reads per tile and block.
-    __device__ __forceinline__ void init(const Prm& p, uint32_t lds_, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_hi_) {
+    // rwave: the wave's 32-row block in the block's rows (its wave index, or wave % 4 when the two groups share rows)
+    __device__ __forceinline__ void init(const Prm& p, uint32_t lds_, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_hi_,
+                                         uint32_t rwave) {
         lane = threadIdx.x & 63u;
         wave = wave_id();
         n = lane & 31u;
         hh = lane >> 5;
         lds = lds_;
         key_hi = key_hi_;
-        row0 = qtile * ROWS + wave * 32u;
+        row0 = qtile * ROWS + rwave * 32u;
         const uint32_t row = row0 + n;
         const uint32_t row_c = min(row, p.S - 1u);
         kfo = n * 128u + ((hh ^ swz(n)) << 4);
@@ -570,12 +573,14 @@ struct Wave {
     __device__ __forceinline__ bool needs_mask(uint32_t key0) const { return key0 + kTile > min(key_hi, lim_wave_min); }
     // keys at or past the range end / causal limit: -1e30 takes no part in the max and converts to P = 0 (pknorm
     // clamps), the reference's two fills (reduce.rs:13-49) in one
-    __device__ __forceinline__ void apply_mask(v16f (&s)[4], uint32_t key0) const {
+    // (accumulator a holds 32-key block KB0 + a of the tile)
+    template <int KB0 = 0, int NA>
+    __device__ __forceinline__ void apply_mask(v16f (&s)[NA], uint32_t key0) const {
         const int nvalid = (int)min(key_hi, lim_row) - (int)key0 - 4 * (int)hh;
 #pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4)
+        for (int t4 = 0; t4 < NA; ++t4)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[t4][i] = (32 * t4 + 8 * (i >> 2) + (i & 3)) < nvalid ? s[t4][i] : -1.0e30f;
+            for (int i = 0; i < 16; ++i) s[t4][i] = (32 * (KB0 + t4) + 8 * (i >> 2) + (i & 3)) < nvalid ? s[t4][i] : -1.0e30f;
     }
 
     // 32-byte K or Q fragment of k-half c (c = 0: d 0..63, 1: d 64..127) of row n of the tile at `base`
@@ -601,7 +606,8 @@ struct Wave {
         const v2i r0 = lds_read_tr8(va), r1 = lds_read_tr8(va + 2048u), r2 = lds_read_tr8(va + 4096u), r3 = lds_read_tr8(va + 6144u);
         return (v8i){r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
     }
-    __device__ __forceinline__ static v8i pfrag(const uint32_t (&pw)[4][4], int j) {
+    template <int NA>
+    __device__ __forceinline__ static v8i pfrag(const uint32_t (&pw)[NA][4], int j) {
         return (v8i){(int)pw[2 * j][0], (int)pw[2 * j][1], (int)pw[2 * j][2], (int)pw[2 * j][3],
                      (int)pw[2 * j + 1][0], (int)pw[2 * j + 1][1], (int)pw[2 * j + 1][2], (int)pw[2 * j + 1][3]};
     }
@@ -646,23 +652,25 @@ struct Wave {
     // S(t+1): k-half 0 of all four 32-key accumulators, then k-half 1 (one Q fragment live at a time). The seed
     // (16 copies of b) is written into s[3] and is the C input of the first MFMA of s[0..2]; s[3] then accumulates
     // in place: no separate seed registers. One K fragment is read one MFMA ahead.
-    __device__ __forceinline__ void qk_all(uint32_t nslot, v16f (&s)[4]) {
+    // (NA accumulators: 32-key blocks KB0 .. KB0 + NA - 1 of the tile)
+    template <int KB0 = 0, int NA>
+    __device__ __forceinline__ void qk_all(uint32_t nslot, v16f (&s)[NA]) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[3][i] = bias;
+        for (int i = 0; i < 16; ++i) s[NA - 1][i] = bias;
         const uint32_t kb = slot_base(lds, kLdsK, nslot, kTileBytes);
         const uint32_t ksb = slot_base(lds, kLdsKs, nslot, (uint32_t)kKsSlot);
-        auto kread = [&](int g) { return frag(kb, g >> 2, 4096u * (g & 3)); };   // g = 4 c + t4
+        auto kread = [&](int g) { return frag(kb, g / NA, 4096u * (uint32_t)(KB0 + g % NA)); };   // g = NA c + t4
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const v8i qf = qfrag(c);
-            v8i kc = kread(4 * c);
+            v8i kc = kread(NA * c);
 #pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) {
-                const int g = 4 * c + t4;
+            for (int t4 = 0; t4 < NA; ++t4) {
+                const int g = NA * c + t4;
                 v8i kn = kc;
-                if (g < 7) kn = kread(g + 1);
-                const uint32_t ksw = kscale(ksb, t4);
-                s[t4] = qk_mfma(kc, qf, c == 0 ? s[3] : s[t4], ksw, c);
+                if (g < 2 * NA - 1) kn = kread(g + 1);
+                const uint32_t ksw = kscale(ksb, KB0 + t4);
+                s[t4] = qk_mfma(kc, qf, c == 0 ? s[NA - 1] : s[t4], ksw, c);
                 kc = kn;
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -682,30 +690,35 @@ struct Wave {
         v8i qf0;
         uint32_t ksw[4];
     };
+    template <int NA = 4, int KB0 = 0>
     __device__ __forceinline__ void qk_prefetch(uint32_t kslot, Ring& ring, QkPre& pre) const {
+        static_assert(DEPTH <= 2 * NA, "the prefetched operands are K fragments");
         const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
         const uint32_t ksb = slot_base(lds, kLdsKs, kslot, (uint32_t)kKsSlot);
 #pragma unroll
-        for (int i = 0; i < DEPTH; ++i) ring[i] = frag(kb, i >> 2, 4096u * (uint32_t)(i & 3));
+        for (int i = 0; i < DEPTH; ++i) ring[i] = frag(kb, i / NA, 4096u * (uint32_t)(KB0 + i % NA));
         pre.qf0 = qfrag(0);
 #pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) pre.ksw[t4] = kscale(ksb, t4);
+        for (int t4 = 0; t4 < NA; ++t4) pre.ksw[t4] = kscale(ksb, KB0 + t4);
     }
 
-    template <bool QK, bool VS = false>
-    __device__ __forceinline__ float m_phase_qf(uint32_t vslot, const uint32_t (&pw)[4][4], uint32_t kslot, v16f (&s)[4], Ring& ring,
+    // NA < 4: the wave's keys are the tile's 32-key blocks KB0 .. KB0 + NA - 1 (NA = 2: one 64-key half; 2 NA QK and
+    // 2 NA PV MFMAs, indices shifted accordingly).
+    template <bool QK, bool VS = false, int KB0 = 0, int NA = 4>
+    __device__ __forceinline__ float m_phase_qf(uint32_t vslot, const uint32_t (&pw)[NA][4], uint32_t kslot, v16f (&s)[NA], Ring& ring,
                                                 const QkPre& pre) {
+        constexpr int NQ = 2 * NA, NI = 4 * NA;   // QK MFMAs, all MFMAs
         const uint32_t vb = slot_base(lds, kLdsV, vslot, kTileBytes);
-        uint32_t vsc[8];   // per-32-key V scales of the 8 PV MFMAs (extension), read a few MFMAs ahead of PV
+        uint32_t vsc[2 * NA];   // per-32-key V scales of the PV MFMAs (extension), read a few MFMAs ahead of PV
         auto read_vs = [&] {
             const uint32_t vsb = slot_base(lds, kLdsVs, vslot, kVsSlot);
 #pragma unroll
-            for (int g = 0; g < 8; ++g) vsc[g] = vscale(vsb, g >> 2, g & 3);
+            for (int g = 0; g < 2 * NA; ++g) vsc[g] = vscale(vsb, KB0 / 2 + (g >> 2), g & 3);
         };
         const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
-        constexpr int I0 = QK ? 0 : 8;
+        constexpr int I0 = QK ? 0 : NQ;
         auto fetch = [&](int i) -> v8i {
-            return i < 8 ? frag(kb, i >> 2, 4096u * (uint32_t)(i & 3)) : vfrag(vb, (i - 8) >> 2, (i - 8) & 3);
+            return i < NQ ? frag(kb, i / NA, 4096u * (uint32_t)(KB0 + i % NA)) : vfrag(vb, KB0 / 2 + ((i - NQ) >> 2), (i - NQ) & 3);
         };
         v8i qf1;
         v8i ones;
@@ -717,27 +730,27 @@ struct Wave {
             if (VS) read_vs();
         }
 #pragma unroll
-        for (int i = I0; i < 16; ++i) {
-            if (i + DEPTH < 16) ring[(i + DEPTH) % (DEPTH + 1)] = fetch(i + DEPTH);
-            if (QK && i == 2) qf1 = qfrag(1);
-            if (QK && i == 5) ones = ones_op();
-            if (VS && QK && i == 4) read_vs();
+        for (int i = I0; i < NI; ++i) {
+            if (i + DEPTH < NI) ring[(i + DEPTH) % (DEPTH + 1)] = fetch(i + DEPTH);
+            if (QK && i == NA - 2) qf1 = qfrag(1);
+            if (QK && i == NQ - 3) ones = ones_op();
+            if (VS && QK && i == NQ - 4) read_vs();
             __builtin_amdgcn_sched_barrier(0);
-            if (i < 8) {
-                const int c = i >> 2, t4 = i & 3;
-                s[t4] = qk_mfma(ring[i % (DEPTH + 1)], c == 0 ? pre.qf0 : qf1, c == 0 ? s[3] : s[t4], pre.ksw[t4], c);
+            if (i < NQ) {
+                const int c = i / NA, t4 = i % NA;
+                s[t4] = qk_mfma(ring[i % (DEPTH + 1)], c == 0 ? pre.qf0 : qf1, c == 0 ? s[NA - 1] : s[t4], pre.ksw[t4], c);
             } else {
-                const int j = (i - 8) >> 2, dc = (i - 8) & 3;
+                const int j = (i - NQ) >> 2, dc = (i - NQ) & 3;
                 const v8i pf = pfrag(pw, j);
                 if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, pf, lacc, 0, 0, 0, 127, 0, 127);
                 o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ring[i % (DEPTH + 1)], pf, o[dc], 0, 0, 0,
-                                                                         VS ? (int)vsc[i - 8] : 127, 0, 127);
+                                                                         VS ? (int)vsc[i - NQ] : 127, 0, 127);
             }
             __builtin_amdgcn_sched_barrier(0);
-            // row max of S(t+1): accumulator (i - 9) behind PV MFMAs 9..12 (accumulator a's last QK MFMA is i = 4 + a)
-            if (QK && i >= 9 && i <= 12) {
+            // row max of S(t+1): accumulator a behind PV MFMA NQ + 1 + a (accumulator a's last QK MFMA is i = NA + a)
+            if (QK && i >= NQ + 1 && i <= NQ + NA) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[i - 9][e]);
+                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[i - NQ - 1][e]);
                 asm volatile("" : "+v"(mx));   // pins this quarter here (the reduction would otherwise sink past the MFMAs)
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -830,17 +843,66 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
     }
 }
 
+// The two key halves of one row block (HV): group B's wave w + 4 writes its softmax state (the 64 O values of each
+// lane as 16 four-value groups, then the row sum and the bias word) to LDS, 16 bytes per lane and group, lane-contiguous,
+// over the dead K/V ring; A's wave w, holding the same rows, reads it and merges: with b the stream's bias (O and l
+// carry a factor 2^(512 b)), the smaller b is kept and the other stream is scaled by 2^(512 (b_min - b)) <= 1. An empty
+// stream (b = 64, O = l = 0) adds zeros. Returns whether the wave goes on to the epilogue (A) or is done (B). Every
+// wave of the block calls it (two block barriers).
+// (Whole v4 groups: stores of single elements extracted from the accumulators were merged by the compiler into
+// ds_write2st64 pairs that repeated one element.)
+template <bool GB, int NT>
+__device__ __forceinline__ bool merge_halves(Wave<NT>& w, uint32_t lds) {
+    constexpr uint32_t kGroups = 17u;   // 16 groups of O values, then (row sum, bias word, -, -)
+    block_barrier();                    // every wave is done with the ring (its copies drained before)
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t base = lds + kLdsK + (wave_id() & 3u) * kGroups * 1024u + lane * 16u;
+    if (GB) {
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const v16f& od = w.o[g >> 2];
+            const v4f x = {od[4 * (g & 3)], od[4 * (g & 3) + 1], od[4 * (g & 3) + 2], od[4 * (g & 3) + 3]};
+            lds_write16(base + (uint32_t)g * 1024u, __builtin_bit_cast(v4i, x));
+        }
+        lds_write16(base + 16u * 1024u, (v4i){__builtin_bit_cast(int, row_sum(w.lacc, lane)), (int)w.bw, 0, 0});
+    }
+    block_barrier();
+    if (GB) return false;
+    const v4i st = lds_read16(base + 16u * 1024u);
+    const uint32_t bw_b = (uint32_t)st[1];
+    const float l_b = __builtin_bit_cast(float, st[0]);
+    const float b_a = bias_of(w.bw), b_b = bias_of(bw_b);
+    const bool keep_a = b_a <= b_b;
+    const float sc = __builtin_amdgcn_exp2f(512.0f * (keep_a ? b_a - b_b : b_b - b_a));
+    const float sa = keep_a ? 1.0f : sc, sb = keep_a ? sc : 1.0f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+        const v4f ob = __builtin_bit_cast(v4f, lds_read16(base + (uint32_t)g * 1024u));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w.o[g >> 2][4 * (g & 3) + e] = __builtin_fmaf(ob[e], sb, w.o[g >> 2][4 * (g & 3) + e] * sa);
+    }
+    const float l = __builtin_fmaf(l_b, sb, row_sum(w.lacc, lane) * sa);
+    w.lacc[0] = l;
+    w.lacc[1] = l;
+    w.bw = keep_a ? w.bw : bw_b;
+    return true;
+}
+
 // Two 4-wave groups one phase apart (waves 0-3: A, 4-7: B; the hardware places waves w and w + 4 on one SIMD).
-// Per tile each wave runs a VALU phase V(t) (row max, rebase, P) and an MFMA phase M(t) (PV(t), then QK(t+1));
-// with B one phase behind A, one wave of every SIMD pair converts while the other multiplies, and s_setprio
-// hands the MFMA-phase wave the issue priority. Between consecutive barriers (global phase f): f = 2t: A V(t),
-// B M(t-1); f = 2t + 1: A M(t), B V(t). Tile u's slot (u % 3) is read in phases 2u-1 .. 2u+2 and must be written
-// before 2u-1: A writes its share of tile t+1 in V(t) (loaded in M(t-1)), B its share of tile t+2 in V(t)
-// (loaded in M(t-1)); every write lands in a slot whose last read phase has passed.
-template <bool LUT, bool SPLIT, bool GB, bool VS>
+// Per tile each wave runs a VALU phase V(t) (rebase, P, the operand prefetch of QK(t+1)) and an MFMA phase M(t)
+// (QK(t+1), then PV(t)); one wave of every SIMD pair converts while the other multiplies, and s_setprio hands the
+// MFMA-phase wave the issue priority. The staging schedule is in the loop below.
+//
+// HV (blocks with at most 128 query rows): both groups take rows 0..127 (wave w and w + 4 the same 32) and split every
+// tile's keys instead, A keys 0..63 and B keys 64..127 (two of the four 32-key accumulators, half the MFMAs); the
+// schedule, the ring and the copies are unchanged. After the loop B hands its softmax state to A through LDS and A
+// merges the two (merge_halves).
+template <bool LUT, bool SPLIT, bool GB, bool VS, bool HV = false>
 __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx,
                                                       uint32_t split, uint32_t key_lo, uint32_t key_hi) {
     constexpr int NT = 512;
+    constexpr int NA = HV ? 2 : 4;              // 32-key accumulators per tile and wave
+    constexpr int KB0 = HV && GB ? 2 : 0;       // the first of them
     const Recipe rc = recipe(LUT);
     const uint32_t tblk = ((bidx * p.splits + split) * p.H + head) * ((p.S + 255u) / 256u) + qtile;
     (void)tblk;
@@ -849,7 +911,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     if (p.trace && (threadIdx.x & 63u) == 0u) p.trace[((size_t)tblk * 8u + (threadIdx.x >> 6)) * 8u + 7u] = p.t_entry;
 #endif
     Wave<NT> w;
-    w.init(p, lds, qtile, head, bidx, key_hi);
+    w.init(p, lds, qtile, head, bidx, key_hi, HV ? wave_id() & 3u : wave_id());
     FMHA_MARK(p, tblk, 1);
     const uint32_t kvh = head / p.gqa;
     const bool causal = (p.flags & 1u) != 0;
@@ -861,58 +923,64 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     st.init(p.k + (size_t)bidx * p.k_b + kvh * kD, p.v + (size_t)bidx * p.v_b + kvh * kD, p.ks + (size_t)bidx * p.ks_b + kvh * 4u,
             p.k_seq, p.SK, lds);
     if (VS) st.init_vs(p.vs32 + (size_t)bidx * p.vs_b + kvh * kD, p.vs_row);
-    auto slot_of = [](uint32_t t) { return t % 3u; };
+    auto slot_of = [](uint32_t t) { return t & 3u; };
     auto key_of = [&](uint32_t t) { return key_lo + t * kTile; };
 
-    v16f s[4];
+    v16f s[NA];
     FMHA_LDECL;
     if (ntiles > 0) {
         // One barrier per tile. Group A (waves 0-3) runs  V(t) | barrier | M(t),  group B (waves 4-7)  V(t) M(t) |
-        // barrier, so between barriers t-1 and t, A runs M(t-1) then V(t) while B runs V(t) then M(t): each SIMD
+        // barrier, so the interval I(t) between barriers t-1 and t holds A: M(t-1), V(t) and B: V(t), M(t): each SIMD
         // holds one wave of each group, and one converts while the other multiplies without a barrier in between.
-        // Staging: V(t) stores the wave's share of K tile t+2 (with its scales) and of V tile t+1, then loads K t+3
-        // and V t+2 (a full iteration ahead of their store). In the interval before barrier t the reads touch K slots
-        // t, t+1 and V slots t-1, t, the writes K slot t+2 and V slot t+1 (mod 3): disjoint, and every read tile was
-        // written before the previous barrier.
-        // K/V tiles go HBM -> LDS by direct copies. V(t) issues K tile t+2 and V tile t+1 into the slots the register-
-        // staged path writes in V(t), with the K-scale words (register-staged, loaded one phase ahead); the barrier that
-        // ends V(t+1) (A) or M(t+1) (B) waits for them (vmcnt counts in issue order: this phase's copies stay in flight).
+        // Reads of tile u: K u in I(u-1) (both prefetches, B's QK) and I(u) (A's QK); V u in I(u) (B) and I(u+1) (A);
+        // the K-scale words of u in I(u-1) only (the prefetch keeps them in registers).
+        // K/V tiles go HBM -> LDS by direct copies: V(t) issues K tile t+3 and V tile t+2 (slot u & 3), and the barrier
+        // that ends I(t+1) waits for them (each wave's vmcnt wait there leaves only the copies of its own V(t+1) in
+        // flight, and the barrier makes every wave's copies visible): the first reads, in I(t+2), come after it. The
+        // slots written in I(t), K (t-1) & 3 and V (t-2) & 3, were last read in I(t-1). The K-scale words go through
+        // registers: V(t) loads tile t+3's and stores tile t+2's (slot (t+2) & 3, last read in I(t-3)), published by
+        // barrier t. A copy past the range (an empty resource) writes zeros into its slot, which is free as above.
         constexpr int kDmaOps = 2 * Stager<NT>::kN + 1 + (VS ? 1 : 0);   // VMEM operations issued per VALU phase
         st.init_dma();
         st.dma(key_of(0), true, 0, key_of(0), true, 0);                 // K 0, V 0
-        st.dma(key_of(1), ntiles > 1, 1, key_of(1), false, 2);          // K 1
-        if (VS) st.dma_vs(key_of(0), true, 0);                          // V scales of tile 0
+        st.dma(key_of(1), ntiles > 1, 1, key_of(1), ntiles > 1, 1);     // K 1, V 1
+        if (VS) {
+            st.dma_vs(key_of(0), true, 0);                              // V scales of tiles 0 and 1
+            st.dma_vs(key_of(1), ntiles > 1, 1);
+        }
         st.load_ks(key_of(0), true);
         st.store_ks(0);
         st.load_ks(key_of(1), ntiles > 1);
         st.store_ks(1);
         st.load_ks(key_of(2), ntiles > 2);
+        st.dma(key_of(2), ntiles > 2, 2, key_of(2), false, 3);          // K 2 (V slot 3 gets zeros, nothing reads it yet)
         w.commit_q();
-        asm volatile("s_waitcnt vmcnt(1)" ::: "memory");   // everything but the K-scale load of tile 2
+        // everything but the K-scale load of tile 2 and the copy of K 2 (both wait for barrier 0)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * Stager<NT>::kN + 1) : "memory");
         FMHA_MARK(p, tblk, 2);
         block_barrier();
         FMHA_MARK(p, tblk, 3);
-        w.qk_all(0, s);
+        w.template qk_all<KB0>(0, s);
         float mrow = row_max(s);   // unmasked row max of the tile the next VALU phase decides on
         {
             typename Wave<NT>::Ring ring;
             typename Wave<NT>::QkPre pre;
-            auto v_phase = [&](uint32_t t, uint32_t (&pw)[4][4], bool last) {
+            auto v_phase = [&](uint32_t t, uint32_t (&pw)[NA][4], bool last) {
                 FMHA_SETPRIO(0);
                 st.store_ks(slot_of(t + 2));
-                st.dma(key_of(t + 2), t + 2 < ntiles, slot_of(t + 2), key_of(t + 1), t + 1 < ntiles, slot_of(t + 1));
-                if (VS) st.dma_vs(key_of(t + 1), t + 1 < ntiles, slot_of(t + 1));
+                st.dma(key_of(t + 3), t + 3 < ntiles, slot_of(t + 3), key_of(t + 2), t + 2 < ntiles, slot_of(t + 2));
+                if (VS) st.dma_vs(key_of(t + 2), t + 2 < ntiles, slot_of(t + 2));
                 st.load_ks(key_of(t + 3), t + 3 < ntiles);
                 if (w.needs_mask(key_of(t))) {
-                    w.apply_mask(s, key_of(t));
+                    w.template apply_mask<KB0>(s, key_of(t));
                     mrow = row_max(s);
                 }
                 rebase<LUT>(rc, mrow, s, w.o, w.lacc, w.bias, w.bw);
 #pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
+                for (int t4 = 0; t4 < NA; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
                 if (!last) {
-                    s[3] = splat16(w.bias);
-                    w.qk_prefetch(slot_of(t + 1), ring, pre);
+                    s[NA - 1] = splat16(w.bias);
+                    w.template qk_prefetch<NA, KB0>(slot_of(t + 1), ring, pre);
                 }
                 FMHA_LMARK(p, tblk, t, 0);
                 // A: the copies of the previous VALU phase have landed; this phase's and the prefetched reads stay in flight
@@ -923,9 +991,9 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
             };
             uint32_t t = 0;
             for (; t + 1 < ntiles; ++t) {
-                uint32_t pw[4][4];
+                uint32_t pw[NA][4];
                 v_phase(t, pw, false);
-                mrow = w.template m_phase_qf<true, VS>(slot_of(t), pw, slot_of(t + 1), s, ring, pre);
+                mrow = w.template m_phase_qf<true, VS, KB0>(slot_of(t), pw, slot_of(t + 1), s, ring, pre);
                 FMHA_LMARK(p, tblk, t, 2);
                 if (GB) block_barrier_keep_dma<0, kDmaOps>();
                 else asm volatile("" ::: "memory");   // A: the compiler-only fence where B has its barrier
@@ -933,9 +1001,9 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
             }
             {
                 // the last tile: PV only
-                uint32_t pw[4][4];
+                uint32_t pw[NA][4];
                 v_phase(t, pw, true);
-                (void)w.template m_phase_qf<false, VS>(slot_of(t), pw, slot_of(t), s, ring, pre);
+                (void)w.template m_phase_qf<false, VS, KB0>(slot_of(t), pw, slot_of(t), s, ring, pre);
                 if (GB) block_barrier();
             }
         }
@@ -944,17 +1012,20 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     }
     FMHA_MARK(p, tblk, 4);
     FMHA_LFLUSH(p, tblk);
+    if (HV) {
+        if (!merge_halves<GB>(w, lds)) return;   // B's state is in A's now
+    }
     epilogue<SPLIT>(p, w, head, bidx, split, rc);
     FMHA_MARK(p, tblk, 5);
 }
 
 // The whole routine is instantiated per group (the groups place their barrier differently; one body with a
 // group-dependent branch, or two loop copies sharing a prologue, made the register allocation spill).
-template <bool LUT, bool SPLIT, bool VS>
+template <bool LUT, bool SPLIT, bool VS, bool HV = false>
 __device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split,
                                 uint32_t key_lo, uint32_t key_hi) {
-    if (wave_id() >= 4u) attend_pingpong_group<LUT, SPLIT, true, VS>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
-    else attend_pingpong_group<LUT, SPLIT, false, VS>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
+    if (wave_id() >= 4u) attend_pingpong_group<LUT, SPLIT, true, VS, HV>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
+    else attend_pingpong_group<LUT, SPLIT, false, VS, HV>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
 }
 
 // One 4-wave group (_t128: one wave per SIMD, so each wave overlaps its own VALU with its own MFMAs): S(t) is
@@ -966,7 +1037,7 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
                                  uint32_t key_hi) {
     const Recipe rc = recipe(LUT);
     Wave<NT> w;
-    w.init(p, lds, qtile, head, bidx, key_hi);
+    w.init(p, lds, qtile, head, bidx, key_hi, wave_id());
     const uint32_t kvh = head / p.gqa;
     const bool causal = (p.flags & 1u) != 0;
     uint32_t key_end = key_hi;
@@ -1138,11 +1209,17 @@ extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvs
     const uint32_t tile_hi = min(ntiles, tile_lo + tps);
     const uint32_t key_lo = tile_lo * 128u, key_hi = min(tile_hi * 128u, p.SK);
     const bool lut = ntiles < 4u;
+    // a block with at most 128 query rows (decode-like S; the ragged last block) splits each tile's keys between the
+    // two wave groups instead of leaving the second group on padding rows (the LUT recipe, SK < 512, keeps the plain
+    // order)
+    const bool hv = !lut && p.S - qt * 256u <= 128u;
     if (p.vs32) {
         if (lut) attend_pingpong<true, true, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+        else if (hv) attend_pingpong<false, true, true, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
         else attend_pingpong<false, true, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
     } else {
         if (lut) attend_pingpong<true, true, false>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+        else if (hv) attend_pingpong<false, true, false, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
         else attend_pingpong<false, true, false>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
     }
 }
@@ -1164,10 +1241,10 @@ extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvspli
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    for (uint32_t s = 0; s < splits; ++s) {
+    // split s's LSE and 8 partial values of this thread
+    auto load = [&](uint32_t s, float& l, float (&x)[8]) {
         const size_t rs = (size_t)s * rows;
-        const float l = lse[rs + row];
-        float x[8];
+        l = lse[rs + row];
         if (f32) {
             const v4f x0 = *(const v4f*)(ohat + ((rs << 4) + t) * 32u), x1 = *(const v4f*)(ohat + ((rs << 4) + t) * 32u + 16u);
 #pragma unroll
@@ -1177,6 +1254,9 @@ extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvspli
 #pragma unroll
             for (int i = 0; i < 4; ++i) { x[2 * i] = h2f((uint32_t)ov[i]); x[2 * i + 1] = h2f((uint32_t)ov[i] >> 16); }
         }
+    };
+    // the streaming LSE-weighted merge (epilogue.rs:89-167), split by split in order
+    auto merge = [&](float l, const float (&x)[8]) {
         const float m_new = fmaxf(m, l);
         const float dm = m_new * -1.0f;
         const float al = __builtin_amdgcn_exp2f(m + dm);
@@ -1185,6 +1265,22 @@ extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvspli
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = acc[i] * al + w * x[i];
         m = m_new;
+    };
+    if (splits <= 8u) {
+        // every split's loads issued before the first merge: one memory latency instead of one per split (indices past
+        // the split count re-read the last split, which is not merged)
+        float l[8], x[8][8];
+#pragma unroll
+        for (uint32_t s = 0; s < 8u; ++s) load(min(s, splits - 1u), l[s], x[s]);
+#pragma unroll
+        for (uint32_t s = 0; s < 8u; ++s)
+            if (s < splits) merge(l[s], x[s]);
+    } else {
+        for (uint32_t s = 0; s < splits; ++s) {
+            float l, x[8];
+            load(s, l, x);
+            merge(l, x);
+        }
     }
     const float rd = __builtin_amdgcn_rcpf(den);
     v4i outv;

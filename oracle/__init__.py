@@ -77,7 +77,7 @@ def lib():
         L.mxo_combine.restype = None
         L.mxo_combine.argtypes = [vp, vp, vp, ctypes.c_long, i]
         L.mxo_emulate_ex.restype = None
-        L.mxo_emulate_ex.argtypes = [ctypes.POINTER(Problem), i, i, vp, vp, vp, i, i]
+        L.mxo_emulate_ex.argtypes = [ctypes.POINTER(Problem), i, i, vp, vp, vp, i, i, i]
         L.mxo_combine_f32.restype = None
         L.mxo_combine_f32.argtypes = [vp, vp, vp, ctypes.c_long, i]
         L.mxo_quant_rows_bf16.argtypes = [vp, ctypes.c_long, f, vp, vp]
@@ -142,10 +142,12 @@ def check_fp64(inp, out_bf16, rows=64, threads=0):
     return lib().mxo_check_fp64(ctypes.byref(p), _ptr(out), int(rows), int(threads)).as_dict()
 
 
-def emulate(inp, splits=0, rows=64, threads=0, partials=False, f32_partials=False):
+def emulate(inp, splits=0, rows=64, threads=0, partials=False, f32_partials=False, split_tiles=False):
     """Bit-level model of the reference kernels on the first ``rows`` rows of every (b, h).
     Returns the bf16 output (uint16, rows not emulated are 0), and with ``partials`` also (ohat, lse f32): ohat fp16
-    (uint16), or f32 with ``f32_partials`` (the FMHA_KVS_F32_PARTIALS extension)."""
+    (uint16), or f32 with ``f32_partials`` (the FMHA_KVS_F32_PARTIALS extension). ``split_tiles`` models the library's
+    order for KV-split blocks of at most 128 query rows (two 64-key streams per tile, merged) instead of the
+    reference's."""
     out = np.zeros(inp.out_elems, np.uint16)
     ohat = lse = None
     if partials and splits:
@@ -154,7 +156,7 @@ def emulate(inp, splits=0, rows=64, threads=0, partials=False, f32_partials=Fals
         lse = np.zeros(splits * rows_total, np.float32)
     p = inp.problem()
     lib().mxo_emulate_ex(ctypes.byref(p), int(splits), int(rows), _ptr(out), _ptr(ohat), _ptr(lse), int(bool(f32_partials)),
-                         int(threads))
+                         int(bool(split_tiles)), int(threads))
     return (out, ohat, lse) if partials else out
 
 

@@ -496,9 +496,10 @@ static float bias_value(uint32_t w) {
 
 /* One query row over keys [klo, khi) (tiles of 128 from klo; keys >= kvis are masked, the
  * key range of this call ends at khi). qd: dequantised-by-MFMA operand (e4m3 values), sq: the
- * two-byte-selected Q scale exponents (qs - 9), per 32-block. */
+ * two-byte-selected Q scale exponents (qs - 9), per 32-block. Only keys [jlo, jhi) of every tile take part
+ * (0, 128 for the reference's order; a 64-key half for one stream of the library's split-tile order, below). */
 static void emulate_row(const mxo_problem* p, const recipe_t* rc, int b, int kvh, const double* qv, const int* sq,
-                        int klo, int khi, int kvis, row_state* st) {
+                        int klo, int khi, int kvis, int jlo, int jhi, row_state* st) {
     pthread_once(&g_once, init_tables);
     st->w = 0x48004800u;
     st->l = 0.0f;
@@ -531,7 +532,7 @@ static void emulate_row(const mxo_problem* p, const recipe_t* rc, int b, int kvh
         /* row max over the valid keys (reduce.rs:52-64; masked keys -1e30, reduce.rs:13-49) */
         float m = -1.0e30f;
         for (int j = 0; j < 128; ++j) {
-            const float x = (t0 + j < vlim) ? s[j] : -1.0e30f;
+            const float x = (t0 + j < vlim && j >= jlo && j < jhi) ? s[j] : -1.0e30f;
             m = fmaxf(m, x);
         }
         const int grow = rc->lazy ? !(rc->thr >= m) : (rc->thr < m);
@@ -563,7 +564,7 @@ static void emulate_row(const mxo_problem* p, const recipe_t* rc, int b, int kvh
             const float x = (t0 + j < vlim) ? s[j] : 0.0f;
             uint16_t u = mxo_pknorm_u16(x);
             if (rc->lut) u = lut_correct(u);
-            pb[j] = mxo_cvt_bf16_fp8(u, rc->conv);
+            pb[j] = (j >= jlo && j < jhi) ? mxo_cvt_bf16_fp8(u, rc->conv) : 0;
             psum += g_e4m3_val[pb[j]];
         }
         st->l = (float)((double)st->l + psum);
@@ -584,6 +585,23 @@ static void emulate_row(const mxo_problem* p, const recipe_t* rc, int b, int kvh
     }
 }
 
+/* The library's split-tile order (extension, no reference counterpart): a KV-split block with at most 128 query rows
+ * (S - 256 floor(i / 256) <= 128) and the non-LUT recipe runs two streams per row, keys 0..63 and 64..127 of every
+ * tile, and merges them: with b the stream's bias (O and l carry 2^(512 b)), the smaller b is kept and the other
+ * stream scaled by 2^(512 (b_min - b)), O = fma(O_b, s_b, O_a s_a) in the order of the kernel's merge. */
+static int split_tile_order(const mxo_problem* p, const recipe_t* rc, int i) {
+    return !rc->lut && p->S - 256 * (i / 256) <= 128;
+}
+static void merge_streams(row_state* a, const row_state* bst) {
+    const float ba = bias_value(a->w), bb = bias_value(bst->w);
+    const int keep_a = ba <= bb;
+    const float sc = exp2f(512.0f * (keep_a ? ba - bb : bb - ba));
+    const float sa = keep_a ? 1.0f : sc, sb = keep_a ? sc : 1.0f;
+    for (int d = 0; d < D; ++d) a->o[d] = fmaf(bst->o[d], sb, a->o[d] * sa);
+    a->l = fmaf(bst->l, sb, a->l * sa);
+    if (!keep_a) a->w = bst->w;
+}
+
 typedef struct {
     const mxo_problem* p;
     int splits, rows;
@@ -591,6 +609,7 @@ typedef struct {
     void* ohat;          /* fp16 rows, or f32 rows when f32_partials */
     float* lse;
     int f32_partials;
+    int split_tiles;     /* 1: the library's split-tile order where it applies (KV split only) */
 } emu_ctx;
 
 static void emu_item(const void* vctx, long item) {
@@ -611,7 +630,7 @@ static void emu_item(const void* vctx, long item) {
     row_state st;
     uint16_t* orow = c->out + (((size_t)b * p->S + i) * p->H + h) * D;
     if (c->splits <= 0) {
-        emulate_row(p, &rc, b, kvh, qv, sq, 0, p->SK, kvis, &st);
+        emulate_row(p, &rc, b, kvh, qv, sq, 0, p->SK, kvis, 0, 128, &st);
         /* state.rs:79-83 (v_rcp_f32, then x v_descale); a row with no visible key (causal extension, S > SK) is 0 */
         const float fin = st.l > 0.0f ? (1.0f / st.l) * vd : 0.0f;
         for (int d = 0; d < D; ++d) orow[d] = mxo_f32_to_bf16(st.o[d] * fin);
@@ -624,7 +643,14 @@ static void emu_item(const void* vctx, long item) {
     for (int s = 0; s < c->splits; ++s) {
         int key_lo, kv_eff;
         mxo_split_range(p->SK, c->splits, s, &key_lo, &kv_eff);
-        emulate_row(p, &rc, b, kvh, qv, sq, key_lo, key_lo + kv_eff, kvis, &st);
+        if (c->split_tiles && split_tile_order(p, &rc, i)) {
+            row_state st_b;
+            emulate_row(p, &rc, b, kvh, qv, sq, key_lo, key_lo + kv_eff, kvis, 0, 64, &st);
+            emulate_row(p, &rc, b, kvh, qv, sq, key_lo, key_lo + kv_eff, kvis, 64, 128, &st_b);
+            merge_streams(&st, &st_b);
+        } else {
+            emulate_row(p, &rc, b, kvh, qv, sq, key_lo, key_lo + kv_eff, kvis, 0, 128, &st);
+        }
         /* block3.rs:291-356 (Ohat = O * v_descale / l, fp16) and softmax.rs:308-322 (lse = log2(l_total) - 2048 (hi + lo)),
          * with l_total = l / 16 (softmax.rs:277-305): the scaled PV form accumulates O / 16 */
         const float l_total = st.l * 0.0625f;
@@ -664,15 +690,15 @@ static void emu_item(const void* vctx, long item) {
 }
 
 void mxo_emulate_ex(const mxo_problem* p, int splits, int rows, uint16_t* out_bf16, void* ohat, float* lse_f32,
-                    int f32_partials, int threads) {
+                    int f32_partials, int split_tiles, int threads) {
     if (rows <= 0 || rows > p->S) rows = p->S;
-    emu_ctx c = {p, splits, rows, out_bf16, ohat, lse_f32, f32_partials};
+    emu_ctx c = {p, splits, rows, out_bf16, ohat, lse_f32, f32_partials, split_tiles};
     run_parallel(threads, (long)p->B * p->H * rows, &c, emu_item);
 }
 
 void mxo_emulate(const mxo_problem* p, int splits, int rows, uint16_t* out_bf16,
                  uint16_t* ohat_f16, float* lse_f32, int threads) {
-    mxo_emulate_ex(p, splits, rows, out_bf16, ohat_f16, lse_f32, 0, threads);
+    mxo_emulate_ex(p, splits, rows, out_bf16, ohat_f16, lse_f32, 0, 0, threads);
 }
 
 /* The combine on f32 partial rows (the FMHA_KVS_F32_PARTIALS extension): the same arithmetic, no fp16 decode. */

@@ -37,9 +37,14 @@ CASES = [
 ]
 
 
-def _emulated_bar(inp, splits):
-    emu = oracle.emulate(inp, splits=splits, rows=ROWS)
-    return emu, oracle.check_fp64(inp, emu, rows=ROWS)
+def _emulated_bar(inp, splits, rows=ROWS, **kw):
+    """The reference's error statistics (its order), and the emulation to compare element-wise with: the library's
+    own order, which differs from the reference's for KV-split blocks of at most 128 query rows (split tiles)."""
+    emu = oracle.emulate(inp, splits=splits, rows=rows, **kw)
+    ref_stats = oracle.check_fp64(inp, emu, rows=rows)
+    if splits:
+        emu = oracle.emulate(inp, splits=splits, rows=rows, split_tiles=True, **kw)
+    return emu, ref_stats
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
@@ -115,8 +120,7 @@ def test_parity_f32_partials(gpu, case):
     out, used, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits, partials="fp32")
     assert used == ("kvsplit", splits)
     out16, _, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits)
-    emu = oracle.emulate(inp, splits=splits, rows=ROWS, f32_partials=True)
-    ref_stats = oracle.check_fp64(inp, emu, rows=ROWS)
+    emu, ref_stats = _emulated_bar(inp, splits, f32_partials=True)
     stats = oracle.check_fp64(inp, out, rows=ROWS)
     stats16 = oracle.check_fp64(inp, out16, rows=ROWS)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, min(ROWS, S))
@@ -150,8 +154,7 @@ def test_parity_v_seq32(gpu, case):
     assert used[0] == path
     used_splits = used[1] if used[0] == "kvsplit" else 0
     rows = min(S, 256 if causal else ROWS)
-    emu = oracle.emulate(inp, splits=used_splits, rows=rows)
-    ref_stats = oracle.check_fp64(inp, emu, rows=rows)
+    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows)
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
     print(f"[case] v_seq32 {name} path={used} ours={stats} emulated={ref_stats} vs-emulation={cmp}", flush=True)
@@ -183,3 +186,36 @@ def test_lse_output(gpu, shape, causal):
     nvis = np.minimum(SK, np.arange(64) + SK - S + 1) if causal else np.full(64, SK)
     many = nvis >= 64
     assert err[:, :, many].mean() < 4e-3
+
+
+# The KV split's split-tile order (blocks of at most 128 query rows: the two wave groups take keys 0..63 and 64..127
+# of every tile and merge at the end), checked on every row, so that the ragged last block of S = 300 and the whole
+# of S <= 128 are in: the bar is the reference's error statistics on those rows, and element-wise closeness to the
+# oracle's emulation of the same order.
+SPLIT_TILE_CASES = [
+    ("S128_SK4096_split4", 1, 8, 8, 128, 4096, 4, {}),
+    ("S300_SK2000_split2", 1, 4, 4, 300, 2000, 2, {}),                 # block 0: plain order, block 1 (44 rows): split
+    ("S1_SK3000_split8", 2, 4, 4, 1, 3000, 8, {}),                      # one row; the last split's tile is ragged
+    ("gqa4_S64_SK1000_split2", 1, 8, 2, 64, 1000, 2, {}),
+    ("S128_SK1200_split4_f32", 1, 4, 4, 128, 1200, 4, {"partials": "fp32"}),
+    ("S100_SK777_split2_vs32", 1, 4, 4, 100, 777, 2, {"v_seq32": True}),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_TILE_CASES, ids=[c[0] for c in SPLIT_TILE_CASES])
+def test_parity_split_tiles(gpu, case):
+    name, B, H, HK, S, SK, splits, opt = case
+    print(f"[case] split tiles {name}", flush=True)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, v_seq32=opt.get("v_seq32", False))
+    f32 = opt.get("partials") == "fp32"
+    out, used, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits, partials=opt.get("partials", "fp16"))
+    assert used == ("kvsplit", splits)
+    emu, ref_stats = _emulated_bar(inp, splits, rows=S, f32_partials=f32)
+    stats = oracle.check_fp64(inp, out, rows=S)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, S)
+    print(f"[case] split tiles {name} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
+    assert not np.isnan(oracle.bf16_to_f32(out)).any()
+    assert stats["bad"] <= ref_stats["bad"]
+    assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"]
+    assert cmp["mean_abs"] <= 0.6 * ref_stats["mean_err"], cmp
+    assert cmp["max_abs"] <= 0.05, cmp

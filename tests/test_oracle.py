@@ -488,3 +488,51 @@ def test_quant_seq32_is_rows_rule_on_transposed_blocks(B, SK, HK):
     assert np.array_equal(s, sr)
     qt = qr.reshape(B, nb, HK, D, 32).transpose(0, 1, 4, 2, 3).reshape(B, nb * 32, HK, D)[:, :SK]
     assert np.array_equal(q.reshape(B, SK, HK, D), qt)
+
+
+def test_split_tile_order_rule():
+    """The split-tile order (extension: the library's KV split on blocks of at most 128 query rows) changes only the
+    rows of such blocks: with S = 300 the rows of block 0 (300 valid rows) are bit-identical to the reference's order,
+    rows 256..299 (44 valid rows) are not; full-sequence emulation ignores the flag."""
+    inp = oracle.Inputs(1, 2, 300, 1000)
+    ref = oracle.emulate(inp, splits=2, rows=0).reshape(1, 300, 2, D)
+    st = oracle.emulate(inp, splits=2, rows=0, split_tiles=True).reshape(ref.shape)
+    np.testing.assert_array_equal(st[:, :256], ref[:, :256])
+    assert (st[:, 256:] != ref[:, 256:]).any()
+    np.testing.assert_array_equal(oracle.emulate(inp, rows=0, split_tiles=True), oracle.emulate(inp, rows=0))
+
+
+def test_split_tile_order_duplicated_halves():
+    """Keys 64..127 of every tile made copies of keys 0..63: the two streams then see the same scores, take the same
+    rebases and merge with scale 1, which doubles O and l; the output equals the reference's order (one stream over
+    the same 128 keys, same maxima, same P) up to the fp32 accumulation order of O and l."""
+    B, H, S, SK = 1, 2, 64, 1024
+    inp = oracle.Inputs(B, H, S, SK)
+    k = inp.k.reshape(B, SK // 128, 128, H, D)
+    v = inp.v.reshape(B, SK // 128, 128, H, D)
+    ks = inp.ks[: B * SK * H * 4].reshape(B, SK // 128, 128, H, 4)
+    k[:, :, 64:] = k[:, :, :64]
+    v[:, :, 64:] = v[:, :, :64]
+    ks[:, :, 64:] = ks[:, :, :64]
+    ref = oracle.bf16_to_f32(oracle.emulate(inp, splits=2, rows=0)).astype(np.float64)
+    st = oracle.bf16_to_f32(oracle.emulate(inp, splits=2, rows=0, split_tiles=True)).astype(np.float64)
+    # one bf16 rounding step (2^-8 relative) at most
+    assert np.all(np.abs(st - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6)
+    assert np.mean(st == ref) > 0.9
+
+
+@pytest.mark.parametrize("boost", [0, 3])
+def test_split_tile_order_accuracy(boost):
+    """Against fp64 attention the split-tile order is as accurate as the reference's (its bar: <= 1.10 x the mean error,
+    no more bad elements). boost = 3 raises the K scales of keys 64..127 of every tile by 3 binades (scores x 8), so
+    the two streams rebase to very different biases and the merge's scaling of one stream by 2^(512 (b_min - b))
+    decides the result: a merge that scaled the wrong stream, or by the inverse factor, fails this."""
+    B, H, S, SK = 1, 4, 128, 2048
+    inp = oracle.Inputs(B, H, S, SK)
+    if boost:
+        ks = inp.ks[: B * SK * H * 4].reshape(B, SK // 128, 128, H, 4)
+        ks[:, :, 64:] += boost
+    ref_stats = oracle.check_fp64(inp, oracle.emulate(inp, splits=4, rows=0), rows=S)
+    st_stats = oracle.check_fp64(inp, oracle.emulate(inp, splits=4, rows=0, split_tiles=True), rows=S)
+    assert st_stats["bad"] <= ref_stats["bad"]
+    assert st_stats["mean_err"] <= 1.10 * ref_stats["mean_err"]
