@@ -65,6 +65,11 @@ constexpr int kVsSlot = 512;
 constexpr int kLdsVs = kLdsKsDummy + 1024;
 constexpr int kLdsVsSink = kLdsVs + kSlots * kVsSlot;
 constexpr int kLdsBytes = kLdsVsSink + 2048;
+// epilogue staging of the output rows (after the loop, over the dead ring): 32 rows of 272 B per wave, above the
+// 68 KiB the split-tile merge uses
+constexpr int kLdsEpi = 68 * 1024;
+constexpr int kEpiRow = 272;
+static_assert(kLdsEpi + 8 * 32 * kEpiRow <= kLdsBytes, "epilogue staging fits");
 
 struct Prm {
     const uint8_t* q;
@@ -366,9 +371,15 @@ struct Stager {
         const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksb + (size_t)kkey0 * ks_row, tile_bytes(kkey0, kvalid, ks_row, 4));
         cur.ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, ksoff, 0, 0);
     }
-    __device__ __forceinline__ void store_ks(uint32_t kslot) const {
+    __device__ __forceinline__ void store_ks(uint32_t kslot) const { store_ks_word(cur.ksr, kslot); }
+    // the same through a register the caller holds (the prologue loads several tiles' words at once)
+    __device__ __forceinline__ uint32_t ks_word(uint32_t kkey0, bool kvalid) const {
+        const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksb + (size_t)kkey0 * ks_row, tile_bytes(kkey0, kvalid, ks_row, 4));
+        return __builtin_amdgcn_raw_buffer_load_b32(rks, ksoff, 0, 0);
+    }
+    __device__ __forceinline__ void store_ks_word(uint32_t word, uint32_t kslot) const {
         const uint32_t ksw_base = tid < 256u ? slot_base(lds, kLdsKs, kslot, kKsSlot) : lds + kLdsKsDummy;
-        lds_write4(ksw_base + kswoff, cur.ksr >> ksshift);
+        lds_write4(ksw_base + kswoff, word >> ksshift);
     }
 
     __device__ __forceinline__ void store_from(const Regs& r, uint32_t kslot, uint32_t vslot) const {
@@ -765,51 +776,47 @@ struct Wave {
 // The row sum of this lane's query (the ones pattern puts it in D dword (lane / 16) % 2).
 __device__ __forceinline__ float row_sum(const v4f& lacc, uint32_t lane) { return ((lane >> 4) & 1u) ? lacc[1] : lacc[0]; }
 
-// Epilogue. Full-sequence kernels: O = O^T . (v_descale / l) -> bf16 rows (state.rs:79-83), 8-byte stores of 4
-// dims; the optional natural-log LSE. KV split: the fp16 partial O-hat = (O / 16) (v_descale / l_total) with
-// l_total = l / 16 and lse = log2(l_total) - 2048 (hi + lo) (block3.rs:291-356, softmax.rs:308-322), partial row
+// Epilogue. Full-sequence kernels: O = O^T . (v_descale / l) -> bf16 rows (state.rs:79-83); the optional natural-log
+// LSE. KV split: the fp16 partial O-hat = (O / 16) (v_descale / l_total) with l_total = l / 16 and
+// lse = log2(l_total) - 2048 (hi + lo) (block3.rs:291-356, softmax.rs:308-322), partial row
 // split * rows_total + (b S + row) H + h. A row with no visible key (causal, S > SK) writes zeros.
+// The 16-bit rows go through LDS: each lane holds 4-dim pieces of one row (the MFMA C layout), so direct stores would
+// touch 32 rows (32 cache lines) per instruction; staged as [32 rows][256 B] per wave, 16 lanes write one row's 256 B
+// with 16-byte stores. `sync`: the ring may still be read by other waves (a block barrier first).
 template <bool SPLIT, int NT>
-__device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32_t head, uint32_t bidx, uint32_t split, const Recipe& rc) {
+__device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32_t head, uint32_t bidx, uint32_t split, const Recipe& rc,
+                                         bool sync) {
     // lane-derived values recomputed here from an opaque lane id: kept from the prologue they would be live (and
     // spilled) across the whole loop
     uint32_t lane;
     asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
-    const uint32_t hh = lane >> 5, row = w.row0 + (lane & 31u);
+    const uint32_t hh = lane >> 5, n = lane & 31u, row = w.row0 + n;
     const float l = row_sum(w.lacc, lane);
-    if (row >= p.S) return;
     const uint32_t dbase = 4u * hh;
+    const bool f32 = SPLIT && p.f32_partials;
+    // per-lane factor and 16-bit conversion of the row pieces
+    float fin;
     if (!SPLIT) {
-        const float fin = l > 0.0f ? __builtin_amdgcn_rcpf(l) * w.vd : 0.0f;
-        // wave-uniform part of the address in SGPRs (readfirstlane), the lane's row on top
-        const uint64_t ob = (uint64_t)(uintptr_t)(p.o + (size_t)bidx * p.o_b + head * 256u);
-        // readfirstlane returns int: both words go through uint32_t, or the low word would sign-extend into the high
-        const uint32_t ob_lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)ob);
-        const uint32_t ob_hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(ob >> 32));
-        uint8_t* obase = (uint8_t*)(uintptr_t)(((uint64_t)ob_hi << 32) | (uint64_t)ob_lo);
-        uint8_t* orow = obase + (size_t)row * p.o_seq;
-#pragma unroll
-        for (int dc = 0; dc < 4; ++dc)
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const v2bf w0 = {(__bf16)(w.o[dc][4 * a] * fin), (__bf16)(w.o[dc][4 * a + 1] * fin)};
-                const v2bf w1 = {(__bf16)(w.o[dc][4 * a + 2] * fin), (__bf16)(w.o[dc][4 * a + 3] * fin)};
-                *(v2i*)(orow + (32 * dc + 8 * a + dbase) * 2) = (v2i){__builtin_bit_cast(int, w0), __builtin_bit_cast(int, w1)};
-            }
-        if (p.lse_out && hh == 0) {
-            // natural-log LSE of the scores (extension): P = 2^(S + 512 b - 127) / conv, l = sum P
-            const float hl = h2f(w.bw) + h2f(w.bw >> 16);
-            const float lse2 = l > 0.0f ? __builtin_amdgcn_logf(l) - hl * 2048.0f + 127.0f + __builtin_amdgcn_logf(rc.conv) - rc.exp2_bias_log2
-                                        : -INFINITY;
-            p.lse_out[((size_t)bidx * p.H + head) * p.S + row] = lse2 * 0.69314718055994531f;
-        }
+        fin = l > 0.0f ? __builtin_amdgcn_rcpf(l) * w.vd : 0.0f;
     } else {
         const float l_total = l * 0.0625f;
-        const float fin = l > 0.0f ? __builtin_amdgcn_rcpf(l_total) * w.vd : 0.0f;
-        const size_t prow = (size_t)split * p.rows_total + ((size_t)bidx * p.S + row) * p.H + head;
-        if (p.f32_partials) {
-            // extension: f32 rows of 512 B (the workspace's rows are fp32-sized either way)
-            uint8_t* orow = p.ohat + prow * 512u;
+        fin = l > 0.0f ? __builtin_amdgcn_rcpf(l_total) * w.vd : 0.0f;
+    }
+    // base of row 0 of this wave's 32 rows and the row stride (bytes), wave-uniform
+    uint8_t* obase;
+    size_t ostride;
+    if (!SPLIT) {
+        obase = p.o + (size_t)bidx * p.o_b + head * 256u + (size_t)w.row0 * p.o_seq;
+        ostride = p.o_seq;
+    } else {
+        const size_t prow0 = (size_t)split * p.rows_total + ((size_t)bidx * p.S + w.row0) * p.H + head;
+        obase = p.ohat + prow0 * (f32 ? 512u : 256u);
+        ostride = (size_t)p.H * (f32 ? 512u : 256u);
+    }
+    if (f32) {
+        // extension: f32 rows of 512 B (the workspace's rows are fp32-sized either way), stored directly
+        if (row < p.S) {
+            uint8_t* orow = obase + (size_t)n * ostride;
 #pragma unroll
             for (int dc = 0; dc < 4; ++dc)
 #pragma unroll
@@ -819,27 +826,51 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
                     for (int e = 0; e < 4; ++e) x[e] = (w.o[dc][4 * a + e] * 0.0625f) * fin;
                     *(v4f*)(orow + (32 * dc + 8 * a + dbase) * 4) = x;
                 }
-        } else {
-            uint8_t* orow = p.ohat + prow * 256u;
+        }
+    } else {
+        if (sync) block_barrier();
+        const uint32_t sbase = w.lds + kLdsEpi + wave_id() * 32u * kEpiRow;
 #pragma unroll
-            for (int dc = 0; dc < 4; ++dc)
+        for (int dc = 0; dc < 4; ++dc)
 #pragma unroll
-                for (int a = 0; a < 4; ++a) {
-                    uint32_t wd[2];
+            for (int a = 0; a < 4; ++a) {
+                uint32_t wd[2];
 #pragma unroll
-                    for (int c = 0; c < 2; ++c) {
-                        const uint32_t lo16 = f2h((w.o[dc][4 * a + 2 * c] * 0.0625f) * fin);
-                        const uint32_t hi16 = f2h((w.o[dc][4 * a + 2 * c + 1] * 0.0625f) * fin);
-                        wd[c] = lo16 | (hi16 << 16);
+                for (int c = 0; c < 2; ++c) {
+                    const float x0 = w.o[dc][4 * a + 2 * c], x1 = w.o[dc][4 * a + 2 * c + 1];
+                    if (!SPLIT) {
+                        const v2bf b = {(__bf16)(x0 * fin), (__bf16)(x1 * fin)};
+                        wd[c] = __builtin_bit_cast(uint32_t, b);
+                    } else {
+                        wd[c] = f2h((x0 * 0.0625f) * fin) | (f2h((x1 * 0.0625f) * fin) << 16);
                     }
-                    *(v2i*)(orow + (32 * dc + 8 * a + dbase) * 2) = (v2i){(int)wd[0], (int)wd[1]};
                 }
+                *(LDS_AS v2i*)(uintptr_t)(sbase + n * kEpiRow + (32 * dc + 8 * a + dbase) * 2) = (v2i){(int)wd[0], (int)wd[1]};
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave reads back only its own rows
+        const uint32_t c16 = lane & 15u;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t r = 4u * k + (lane >> 4);
+            const v4i x = lds_read16(sbase + r * kEpiRow + c16 * 16u);
+            if (w.row0 + r < p.S) *(v4i*)(obase + (size_t)r * ostride + c16 * 16u) = x;
         }
-        if (hh == 0) {
+    }
+    if (row >= p.S || hh != 0) return;
+    if (!SPLIT) {
+        if (p.lse_out) {
+            // natural-log LSE of the scores (extension): P = 2^(S + 512 b - 127) / conv, l = sum P
             const float hl = h2f(w.bw) + h2f(w.bw >> 16);
-            // an empty range (l = 0) gets -1e30: the combine gives it weight 0
-            p.lse[prow] = l > 0.0f ? __builtin_amdgcn_logf(l_total) + (hl * 2048.0f) * -1.0f : -1.0e30f;
+            const float lse2 = l > 0.0f ? __builtin_amdgcn_logf(l) - hl * 2048.0f + 127.0f + __builtin_amdgcn_logf(rc.conv) - rc.exp2_bias_log2
+                                        : -INFINITY;
+            p.lse_out[((size_t)bidx * p.H + head) * p.S + row] = lse2 * 0.69314718055994531f;
         }
+    } else {
+        const float l_total = l * 0.0625f;
+        const float hl = h2f(w.bw) + h2f(w.bw >> 16);
+        const size_t prow = (size_t)split * p.rows_total + ((size_t)bidx * p.S + row) * p.H + head;
+        // an empty range (l = 0) gets -1e30: the combine gives it weight 0
+        p.lse[prow] = l > 0.0f ? __builtin_amdgcn_logf(l_total) + (hl * 2048.0f) * -1.0f : -1.0e30f;
     }
 }
 
@@ -941,22 +972,24 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
         // registers: V(t) loads tile t+3's and stores tile t+2's (slot (t+2) & 3, last read in I(t-3)), published by
         // barrier t. A copy past the range (an empty resource) writes zeros into its slot, which is free as above.
         constexpr int kDmaOps = 2 * Stager<NT>::kN + 1 + (VS ? 1 : 0);   // VMEM operations issued per VALU phase
+        // Every prologue load goes out at once (Q and its scales were issued by init): the K-scale words of tiles 0..2,
+        // then the copies. One memory round trip to the first barrier (the stores of the words wait for their loads).
         st.init_dma();
+        const uint32_t ks0 = st.ks_word(key_of(0), true);
+        const uint32_t ks1 = st.ks_word(key_of(1), ntiles > 1);
+        st.load_ks(key_of(2), ntiles > 2);                              // stored by V(0)
+        // The first barrier needs K 0, V 0 and K 1 (read in I(0)); V 1 and K 2 are first read in I(1), so barrier 0
+        // waits for them and they stay out of the first barrier's burst.
         st.dma(key_of(0), true, 0, key_of(0), true, 0);                 // K 0, V 0
-        st.dma(key_of(1), ntiles > 1, 1, key_of(1), ntiles > 1, 1);     // K 1, V 1
-        if (VS) {
-            st.dma_vs(key_of(0), true, 0);                              // V scales of tiles 0 and 1
-            st.dma_vs(key_of(1), ntiles > 1, 1);
-        }
-        st.load_ks(key_of(0), true);
-        st.store_ks(0);
-        st.load_ks(key_of(1), ntiles > 1);
-        st.store_ks(1);
-        st.load_ks(key_of(2), ntiles > 2);
-        st.dma(key_of(2), ntiles > 2, 2, key_of(2), false, 3);          // K 2 (V slot 3 gets zeros, nothing reads it yet)
+        st.dma(key_of(1), ntiles > 1, 1, key_of(1), false, 3);          // K 1 (V slot 3 gets zeros, nothing reads it yet)
+        if (VS) st.dma_vs(key_of(0), true, 0);                          // V scales of tile 0
+        st.dma(key_of(2), ntiles > 2, 2, key_of(1), ntiles > 1, 1);     // K 2, V 1
+        if (VS) st.dma_vs(key_of(1), ntiles > 1, 1);                    // V scales of tile 1
+        st.store_ks_word(ks0, 0);
+        st.store_ks_word(ks1, 1);
         w.commit_q();
-        // everything but the K-scale load of tile 2 and the copy of K 2 (both wait for barrier 0)
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * Stager<NT>::kN + 1) : "memory");
+        // everything but the copies of K 2 and V 1 (which barrier 0 waits for)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * Stager<NT>::kN + (VS ? 1 : 0)) : "memory");
         FMHA_MARK(p, tblk, 2);
         block_barrier();
         FMHA_MARK(p, tblk, 3);
@@ -1015,7 +1048,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     if (HV) {
         if (!merge_halves<GB>(w, lds)) return;   // B's state is in A's now
     }
-    epilogue<SPLIT>(p, w, head, bidx, split, rc);
+    epilogue<SPLIT>(p, w, head, bidx, split, rc, !HV);   // HV: the merge's barriers already retired the ring
     FMHA_MARK(p, tblk, 5);
 }
 
@@ -1118,7 +1151,7 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
             w.template pv_all<VS>(slot, pw);
         }
     }
-    epilogue<false>(p, w, head, bidx, 0, rc);
+    epilogue<false>(p, w, head, bidx, 0, rc, true);
 }
 
 // Workgroup -> (q tile, head, z): consecutive tiles of one (batch, head) land on one XCD, so each XCD's L2 holds the K/V
