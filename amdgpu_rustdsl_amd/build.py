@@ -10,6 +10,7 @@ Outputs (in-tree, git-ignored, shipped with the source tree):
 """
 import os
 import subprocess
+import tempfile
 import sys
 
 PKG = os.path.dirname(os.path.abspath(__file__))
@@ -35,11 +36,29 @@ def _run(cmd):
     return r
 
 
+def code_object_calls(hsaco):
+    """Call instructions in the gfx950 code object inside a --genco bundle (the kernels must be one function each:
+    in an outlined callee the kernel-argument pointer is not an ABI input and compiles to null, so its first
+    argument read faults). Returns the offending lines."""
+    llvm = os.path.join(ROCM, "llvm", "bin")
+    with tempfile.TemporaryDirectory() as td:
+        co = os.path.join(td, "k.co")
+        _run([os.path.join(llvm, "clang-offload-bundler"), "--unbundle", "--type=o", "--input=" + hsaco,
+              "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", "--output=" + co])
+        dis = _run([os.path.join(llvm, "llvm-objdump"), "-d", "--no-show-raw-insn", co]).stdout
+    return [l.strip() for l in dis.splitlines() if "s_swappc_b64" in l or "s_call_b64" in l]
+
+
 def build(verbose=False):
     os.makedirs(OUT, exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     _run([hipcc, *HIP_FLAGS, "--genco", os.path.join(CSRC, "fmha_kernels.hip"), "-o", HSACO])
     _run([hipcc, *HIP_FLAGS, "--genco", os.path.join(CSRC, "quant_kernels.hip"), "-o", QHSACO])
+    for co in (HSACO, QHSACO):
+        calls = code_object_calls(co)
+        if calls:
+            os.remove(co)
+            raise RuntimeError(f"{co}: a kernel calls an outlined function ({calls[0]}); force-inline it")
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
           "-I" + os.path.join(ROCM, "include"), '-DFMHA_HSACO_PATH="%s"' % HSACO, '-DMXQ_HSACO_PATH="%s"' % QHSACO,
           os.path.join(CSRC, "fmha_host.cpp"), os.path.join(CSRC, "quant_host.cpp"), "-L" + os.path.join(ROCM, "lib"), "-lamdhip64",

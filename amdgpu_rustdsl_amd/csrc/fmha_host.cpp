@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 
@@ -75,15 +76,19 @@ namespace {
 using fmha_internal::fail;
 using fmha_internal::set_err;
 
-const char* const kKernelNames[4] = {
+const char* const kKernelNames[7] = {
     "fmha_fwd_hd128_mxfp8_v3_vs128",
     "fmha_fwd_hd128_mxfp8_v3_t128",
     "fmha_fwd_hd128_mxfp8_v3_kvsplit",
     "fmha_fwd_hd128_mxfp8_v3_kvsplit_combine8h",
+    // extension kernels: the softmax scale at 0x050 applied in the kernel (FMHA_FLAG_SCALE / FMHA_KVS_SCALE)
+    "fmha_fwd_hd128_mxfp8_v3_vs128_scaled",
+    "fmha_fwd_hd128_mxfp8_v3_t128_scaled",
+    "fmha_fwd_hd128_mxfp8_v3_kvsplit_scaled",
 };
-enum { K_VS128 = 0, K_T128 = 1, K_KVSPLIT = 2, K_COMBINE = 3 };
+enum { K_VS128 = 0, K_T128 = 1, K_KVSPLIT = 2, K_COMBINE = 3, K_VS128_SC = 4, K_T128_SC = 5, K_KVSPLIT_SC = 6 };
 
-fmha_internal::ModuleCache<4> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
+fmha_internal::ModuleCache<7> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
 
 int get_functions(hipFunction_t** out, char* err, size_t errlen) { return g_fmha.get(out, err, errlen); }
 
@@ -150,13 +155,28 @@ int rules_grid(const fmha_mxfp8_args& a, uint32_t gx, uint32_t gy, int rows_per_
     return FMHA_OK;
 }
 
+// The in-kernel softmax scale (FMHA_FLAG_SCALE / FMHA_KVS_SCALE): c = f32(scale log2 e) must be a positive normal f32
+// (its exponent then splits off exactly, and the Q scale exponents shift by it)
+bool scale_ok(float scale) {
+    const float c = scale * 1.44269504088896340736f;
+    return std::isfinite(c) && std::isnormal(c) && c > 0.0f;
+}
+int rules_scale(const fmha_mxfp8_args& a, bool on, char* err, size_t errlen) {
+    float scale;
+    std::memcpy(&scale, &a.softmax_scale, 4);
+    if (on && !scale_ok(scale))
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x50) outside contract (softmax scale)");
+    return FMHA_OK;
+}
+
 int validate_base(const fmha_mxfp8_args& a, const fmha_mxfp8_buffer_sizes& sz, uint32_t gx, uint32_t gy, i64 B, i64 HK,
                   int rows_per_block, char* err, size_t errlen) {
     int rc;
     if ((rc = rules_extent(a, sz, B, (a.flags & FMHA_FLAG_V_SEQ32) != 0, err, errlen)) != FMHA_OK) return rc;
     if ((rc = rules_range(a, err, errlen)) != FMHA_OK) return rc;
-    if ((a.flags & ~(FMHA_FLAG_CAUSAL | FMHA_FLAG_V_SEQ32)) != 0)
+    if ((a.flags & ~(FMHA_FLAG_CAUSAL | FMHA_FLAG_V_SEQ32 | FMHA_FLAG_SCALE)) != 0)
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x280) outside contract");
+    if ((rc = rules_scale(a, (a.flags & FMHA_FLAG_SCALE) != 0, err, errlen)) != FMHA_OK) return rc;
     if ((rc = rules_is(a, HK, err, errlen)) != FMHA_OK) return rc;
     return rules_grid(a, gx, gy, rows_per_block, err, errlen);
 }
@@ -202,8 +222,9 @@ int fmha_mxfp8_validate_kvsplit(const fmha_mxfp8_kvsplit_args* ka, const fmha_mx
     if (sz->ptr_ohat < (uint64_t)(splits * rows * row_bytes)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_ohat: buffer ptr_ohat smaller than declared allocation");
     if (sz->ptr_lse < (uint64_t)(splits * rows * 4)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_lse: buffer ptr_lse smaller than declared allocation");
     if ((rc = rules_range(a, err, errlen)) != FMHA_OK) return rc;
-    if (splits < 1 || (ka->kvs_splits & ~(0xffffu | FMHA_KVS_F32_PARTIALS | FMHA_KVS_V_SEQ32)) != 0)
+    if (splits < 1 || (ka->kvs_splits & ~(0xffffu | FMHA_KVS_F32_PARTIALS | FMHA_KVS_V_SEQ32 | FMHA_KVS_SCALE)) != 0)
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x280) outside contract");
+    if ((rc = rules_scale(a, (ka->kvs_splits & FMHA_KVS_SCALE) != 0, err, errlen)) != FMHA_OK) return rc;
     if (rows < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x284) outside contract");
     if ((rc = rules_is(a, HK, err, errlen)) != FMHA_OK) return rc;
     if (rows != B * (i64)a.s_seq_len * (i64)a.s_q_head_num) return fail(err, errlen, FMHA_ERR_KA_IS, "GV-HOST-KA-IS", "ka(0x284) relation failed");
@@ -287,13 +308,13 @@ size_t fmha_mxfp8_workspace_bytes(int64_t B, int64_t H, int64_t S, int splits) {
 }
 
 int fmha_mxfp8_launch_vs128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream) {
-    return launch_raw(K_VS128, a, sizeof(*a), gx, gy, gz, 512, stream, nullptr, 0);
+    return launch_raw((a->flags & FMHA_FLAG_SCALE) ? K_VS128_SC : K_VS128, a, sizeof(*a), gx, gy, gz, 512, stream, nullptr, 0);
 }
 int fmha_mxfp8_launch_t128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream) {
-    return launch_raw(K_T128, a, sizeof(*a), gx, gy, gz, 256, stream, nullptr, 0);
+    return launch_raw((a->flags & FMHA_FLAG_SCALE) ? K_T128_SC : K_T128, a, sizeof(*a), gx, gy, gz, 256, stream, nullptr, 0);
 }
 int fmha_mxfp8_launch_kvsplit(const fmha_mxfp8_kvsplit_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream) {
-    return launch_raw(K_KVSPLIT, a, sizeof(*a), gx, gy, gz, 512, stream, nullptr, 0);
+    return launch_raw((a->kvs_splits & FMHA_KVS_SCALE) ? K_KVSPLIT_SC : K_KVSPLIT, a, sizeof(*a), gx, gy, gz, 512, stream, nullptr, 0);
 }
 int fmha_mxfp8_launch_combine(const fmha_mxfp8_combine_args* a, uint32_t gx, void* stream) {
     return launch_raw(K_COMBINE, a, sizeof(*a), gx, 1, 1, 256, stream, nullptr, 0);
@@ -326,9 +347,13 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "f32_partials must be 0 or 1");
     if (p->v_seq32 != 0 && p->v_seq32 != 1)
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "v_seq32 must be 0 or 1");
+    const bool scaled = p->softmax_scale != 0.0f;
+    if (scaled && !scale_ok(p->softmax_scale))
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "softmax_scale must be 0 or positive with a normal f32 scale x log2(e)");
     fmha_mxfp8_args a;
     fmha_mxfp8_fill_args(&a, p->o, p->q, p->k, p->v, p->q_descale, p->k_descale, p->v_descale, (int)B, (int)H, (int)HK, (int)S, (int)SK);
-    a.flags = (p->causal ? FMHA_FLAG_CAUSAL : 0u) | (p->v_seq32 ? FMHA_FLAG_V_SEQ32 : 0u);
+    a.flags = (p->causal ? FMHA_FLAG_CAUSAL : 0u) | (p->v_seq32 ? FMHA_FLAG_V_SEQ32 : 0u) | (scaled ? FMHA_FLAG_SCALE : 0u);
+    if (scaled) std::memcpy(&a.softmax_scale, &p->softmax_scale, 4);
     fmha_mxfp8_buffer_sizes sz;
     std::memset(&sz, 0, sizeof(sz));
     sz.ptr_q = p->bytes_q; sz.ptr_k = p->bytes_k; sz.ptr_v = p->bytes_v; sz.ptr_o = p->bytes_o;
@@ -343,7 +368,8 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
         int rc = path == FMHA_PATH_VS128 ? fmha_mxfp8_validate_vs128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen)
                                          : fmha_mxfp8_validate_t128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen);
         if (rc != FMHA_OK) return rc;
-        return launch_raw(path == FMHA_PATH_VS128 ? K_VS128 : K_T128, &a, sizeof(a), gx, gy, (uint32_t)B, (uint32_t)(rows * 2), stream,
+        const int kern = path == FMHA_PATH_VS128 ? (scaled ? K_VS128_SC : K_VS128) : (scaled ? K_T128_SC : K_T128);
+        return launch_raw(kern, &a, sizeof(a), gx, gy, (uint32_t)B, (uint32_t)(rows * 2), stream,
                           err, errlen);
     }
     // KV split: partials (fp32-sized rows, as ref_host.cpp:149 / ops.py:133) then the LSE, both in the workspace
@@ -360,14 +386,14 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     ka.ptr_ohat = ohat;
     ka.ptr_lse = lse;
     const uint32_t part_fmt = p->f32_partials ? FMHA_KVS_F32_PARTIALS : 0u;
-    ka.kvs_splits = (uint32_t)splits | part_fmt | (p->v_seq32 ? FMHA_KVS_V_SEQ32 : 0u);
+    ka.kvs_splits = (uint32_t)splits | part_fmt | (p->v_seq32 ? FMHA_KVS_V_SEQ32 : 0u) | (scaled ? FMHA_KVS_SCALE : 0u);
     ka.kvs_rows_total = (uint32_t)rows_total;
     sz.ptr_ohat = (uint64_t)splits * rows_total * 512;
     sz.ptr_lse = (uint64_t)splits * rows_total * 4;
     const uint32_t gx = (uint32_t)((S + 255) / 256), gz = (uint32_t)(B * splits);
     int rc = fmha_mxfp8_validate_kvsplit(&ka, &sz, gx, gy, gz, B, HK, 0, err, errlen);
     if (rc != FMHA_OK) return rc;
-    rc = launch_raw(K_KVSPLIT, &ka, sizeof(ka), gx, gy, gz, 512, stream, err, errlen);
+    rc = launch_raw(scaled ? K_KVSPLIT_SC : K_KVSPLIT, &ka, sizeof(ka), gx, gy, gz, 512, stream, err, errlen);
     if (rc != FMHA_OK) return rc;
     fmha_mxfp8_combine_args ca;
     ca.ptr_ohat = ohat;

@@ -90,6 +90,12 @@ struct Prm {
     // 32-key block, vs_b = ceil(SK/32) vs_row per batch) and the per-tensor descale is 1
     const uint8_t* vs32;
     uint32_t vs_row, vs_b;
+    // extension: the softmax scale applied in the kernel. c = f32(scale log2 e) = 2^qk_e qk_m, qk_m in [1, 2): qk_e
+    // is added to the Q scale exponents, S is seeded with b qk_rm (qk_rm = 1 / qk_m) and multiplied by qk_m. Without
+    // the extension qk_e = 0 and qk_m = qk_rm = 1 (the seed is b, exactly).
+    float qk_m, qk_rm;
+    int32_t qk_e;
+    uint32_t qk_scaled;
 #ifdef FMHA_TRACE
     uint64_t* trace;   // debug builds only: per (block, wave) timestamps, pointer at kernarg 0x288
     uint64_t t_entry;  // timestamp of the kernel's first instruction
@@ -138,6 +144,22 @@ __device__ inline T ka(uint32_t off) {
 }
 #define KA_FIELD(T, field) ka<T>(offsetof(fmha_mxfp8_args, field))
 
+// c = f32(softmax scale (kernarg 0x050) x log2 e) split into 2^e m (the host checked that it is a positive normal)
+__device__ inline void set_qk_scale(Prm& p, bool on) {
+    p.qk_scaled = on ? 1u : 0u;
+    p.qk_e = 0;
+    p.qk_m = p.qk_rm = 1.0f;
+    if (!on) return;
+    const float c = ka<float>(0x050) * 1.44269504088896340736f;
+    const uint32_t u = __builtin_bit_cast(uint32_t, c);
+    p.qk_e = (int32_t)((u >> 23) & 0xffu) - 127;
+    p.qk_m = __builtin_bit_cast(float, (u & 0x007fffffu) | (127u << 23));
+    p.qk_rm = 1.0f / p.qk_m;
+}
+
+// SC: the `_scaled` kernels, which apply the softmax scale at 0x050; the reference-named kernels fold qk_m = qk_rm = 1,
+// qk_e = 0 as constants (their code carries nothing of the extension).
+template <bool SC = false>
 __device__ inline Prm prm_from_kernarg() {
     Prm p;
     p.q = (const uint8_t*)KA_FIELD(uint64_t, ptr_q); p.k = (const uint8_t*)KA_FIELD(uint64_t, ptr_k);
@@ -155,6 +177,7 @@ __device__ inline Prm prm_from_kernarg() {
     p.vs_row = p.k_seq;
     p.vs_b = ((p.SK + 31u) >> 5) * p.vs_row;
     p.ohat = nullptr; p.lse = nullptr; p.splits = 1; p.rows_total = 0; p.f32_partials = 0;
+    set_qk_scale(p, SC);
 #ifdef FMHA_TRACE
     p.trace = (uint64_t*)(uintptr_t)(ka<uint32_t>(0x288) | ((uint64_t)ka<uint32_t>(0x28C) << 32));
 #endif
@@ -440,8 +463,10 @@ __device__ __forceinline__ float row_max(const v16f (&s)[NA]) {
 
 // The rebase decision of one tile given its row max m: when any lane's max passes the threshold, the new two-word
 // reference and the rescale of S, O and the row sums (lanes below the threshold keep their reference, delta = 0).
+// (bias: the seed of S, b rm; rm = 1 unless the softmax scale is applied in the kernel)
 template <bool LUT, int NA>
-__device__ __forceinline__ void rebase(const Recipe& rc, float m, v16f (&s)[NA], v16f (&o)[4], v4f& lacc, float& bias, uint32_t& bw) {
+__device__ __forceinline__ void rebase(const Recipe& rc, float m, v16f (&s)[NA], v16f (&o)[4], v4f& lacc, float& bias, uint32_t& bw,
+                                       float rm) {
     // softmax.rs:125-160 eager: thr < m; softmax.rs:186-241 lazy: !(thr >= m), which also takes NaN
     const bool grow = LUT ? (rc.thr < m) : !(rc.thr >= m);
     if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -469,7 +494,7 @@ __device__ __forceinline__ void rebase(const Recipe& rc, float m, v16f (&s)[NA],
             for (int i = 0; i < 16; ++i) o[dc][i] *= corr;
 #pragma unroll
         for (int i = 0; i < 4; ++i) lacc[i] *= corr;
-        bias = bias_of(bw);
+        bias = bias_of(bw) * rm;
     }
 }
 
@@ -515,7 +540,10 @@ struct Wave {
     uint32_t lim_row, lim_wave_min, lim_wave_max, key_hi;
     // softmax state
     uint32_t bw;       // two f16 words (hi = low half); b = 64 makes tile 0 rebase
-    float bias;        // b of this lane's query: the seed of every S accumulator
+    float bias;        // the seed of every S accumulator: b of this lane's query (times qrm)
+    // the softmax scale applied in the kernel (extension): S' = qm (S + b qrm), the Q scale exponents shifted by qe
+    float qm, qrm;
+    int32_t qe;
     v16f o[4];
     v4f lacc;
     v4i qtmp[4];       // the lane's Q bytes (32 B of the k-half c = 0 and 32 B of c = 1), resident for the whole range
@@ -525,7 +553,7 @@ struct Wave {
     __device__ __forceinline__ void commit_q() {
         // Q scale bytes of the two k-halves (E8M0 - 9: S comes out x 2^-9)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) sq[c] = (int)(((qsw >> (8 * (2 * c + hh))) - 9u) & 0xffu);
+        for (int c = 0; c < 2; ++c) sq[c] = (int)(((qsw >> (8 * (2 * c + hh))) - 9u + (uint32_t)qe) & 0xffu);
     }
 
     // Lane constants, softmax state, and the loads of the lane's Q bytes and scales. The Q bytes stay in registers
@@ -571,8 +599,11 @@ struct Wave {
         // ones pattern of the row-sum MFMA (16x16x128): lane la holds A row la % 16, k-groups la / 16; row m sums
         // the P bytes of query (m % 2 ? n + 16 : n) -> ones iff (la / 16) % 2 == la % 2
         onew = (((lane >> 4) & 1u) == (lane & 1u)) ? 0x38383838u : 0u;
+        qm = p.qk_m;
+        qrm = p.qk_rm;
+        qe = p.qk_e;
         bw = 0x48004800u;
-        bias = bias_of(bw);
+        bias = bias_of(bw) * qrm;
 #pragma unroll
         for (int dc = 0; dc < 4; ++dc)
 #pragma unroll
@@ -582,6 +613,16 @@ struct Wave {
 
     __device__ __forceinline__ bool active(uint32_t key0) const { return key0 < lim_wave_max; }
     __device__ __forceinline__ bool needs_mask(uint32_t key0) const { return key0 + kTile > min(key_hi, lim_wave_min); }
+    // S' = qm S_acc (S_acc seeded with b qrm) when the softmax scale is applied in the kernel; a row max taken before
+    // scales the same way (qm > 0 and rounding are monotonic).
+    template <int NA>
+    __device__ __forceinline__ void scale_s(v16f (&s)[NA], float& m) const {
+#pragma unroll
+        for (int t4 = 0; t4 < NA; ++t4)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[t4][i] *= qm;
+        m *= qm;
+    }
     // keys at or past the range end / causal limit: -1e30 takes no part in the max and converts to P = 0 (pknorm
     // clamps), the reference's two fills (reduce.rs:13-49) in one
     // (accumulator a holds 32-key block KB0 + a of the tile)
@@ -928,7 +969,7 @@ __device__ __forceinline__ bool merge_halves(Wave<NT>& w, uint32_t lds) {
 // tile's keys instead, A keys 0..63 and B keys 64..127 (two of the four 32-key accumulators, half the MFMAs); the
 // schedule, the ring and the copies are unchanged. After the loop B hands its softmax state to A through LDS and A
 // merges the two (merge_halves).
-template <bool LUT, bool SPLIT, bool GB, bool VS, bool HV = false>
+template <bool LUT, bool SPLIT, bool GB, bool VS, bool HV, bool SC>
 __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx,
                                                       uint32_t split, uint32_t key_lo, uint32_t key_hi) {
     constexpr int NT = 512;
@@ -1004,11 +1045,12 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
                 st.dma(key_of(t + 3), t + 3 < ntiles, slot_of(t + 3), key_of(t + 2), t + 2 < ntiles, slot_of(t + 2));
                 if (VS) st.dma_vs(key_of(t + 2), t + 2 < ntiles, slot_of(t + 2));
                 st.load_ks(key_of(t + 3), t + 3 < ntiles);
+                if (SC) w.scale_s(s, mrow);   // the in-kernel softmax scale (an instantiation of its own)
                 if (w.needs_mask(key_of(t))) {
                     w.template apply_mask<KB0>(s, key_of(t));
                     mrow = row_max(s);
                 }
-                rebase<LUT>(rc, mrow, s, w.o, w.lacc, w.bias, w.bw);
+                rebase<LUT>(rc, mrow, s, w.o, w.lacc, w.bias, w.bw, w.qrm);
 #pragma unroll
                 for (int t4 = 0; t4 < NA; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
                 if (!last) {
@@ -1054,19 +1096,19 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
 
 // The whole routine is instantiated per group (the groups place their barrier differently; one body with a
 // group-dependent branch, or two loop copies sharing a prologue, made the register allocation spill).
-template <bool LUT, bool SPLIT, bool VS, bool HV = false>
-__device__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split,
+template <bool LUT, bool SPLIT, bool VS, bool HV, bool SC>
+__device__ __forceinline__ void attend_pingpong(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t split,
                                 uint32_t key_lo, uint32_t key_hi) {
-    if (wave_id() >= 4u) attend_pingpong_group<LUT, SPLIT, true, VS, HV>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
-    else attend_pingpong_group<LUT, SPLIT, false, VS, HV>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
+    if (wave_id() >= 4u) attend_pingpong_group<LUT, SPLIT, true, VS, HV, SC>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
+    else attend_pingpong_group<LUT, SPLIT, false, VS, HV, SC>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
 }
 
 // One 4-wave group (_t128: one wave per SIMD, so each wave overlaps its own VALU with its own MFMAs): S(t) is
 // computed and decided one iteration ahead. Iteration t: [P(t) conversion | QK(t+1)] then [PV(t) | row max of
 // S(t+1)]; the tile t+2 staged through registers lands in slot (t+2) % 3 (tile t-1's: its last read was in
 // iteration t-1), one barrier, then the rebase decision of tile t+1. The last tile runs [P | PV] alone.
-template <bool LUT, bool VS, int NT = 256>
-__device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_lo,
+template <bool LUT, bool VS, bool SC, int NT = 256>
+__device__ __forceinline__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_lo,
                                  uint32_t key_hi) {
     const Recipe rc = recipe(LUT);
     Wave<NT> w;
@@ -1100,8 +1142,10 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
         block_barrier();
         if (w.active(key_of(0))) {
             w.qk_all(0, s);
+            float m0 = 0.0f;
+            if (SC) w.scale_s(s, m0);
             if (w.needs_mask(key_of(0))) w.apply_mask(s, key_of(0));
-            rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw);
+            rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw, w.qrm);
         }
         uint32_t slot = 0;
         for (uint32_t t = 0; t + 1 < ntiles; ++t) {
@@ -1135,13 +1179,14 @@ __device__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uin
             if (act) w.template pv_all<VS>(slot, pw);
             float m = 0.0f;
             if (act_next) {
+                if (SC) w.scale_s(s, m);
                 if (w.needs_mask(key_of(t + 1))) w.apply_mask(s, key_of(t + 1));
                 m = row_max(s);
             }
             if (t + 2 < ntiles) st.store(sslot, sslot);
             if (VS && t + 2 < ntiles) st.store_vs(vs2, sslot);
             block_barrier();
-            if (act_next) rebase<LUT>(rc, m, s, w.o, w.lacc, w.bias, w.bw);
+            if (act_next) rebase<LUT>(rc, m, s, w.o, w.lacc, w.bias, w.bw, w.qrm);
             slot = nslot;
         }
         if (w.active(key_of(ntiles - 1))) {
@@ -1170,59 +1215,44 @@ __device__ inline void block_coords(uint32_t S, uint32_t H, uint32_t rows, uint3
     z = blockIdx.z;
 }
 
-template <int NT>
-__device__ void full_kernel(uint32_t lds) {
+// Inlined into its kernel, like everything that reads the kernel arguments: in a called (outlined) function the
+// kernarg segment pointer is not an ABI input and compiles to null. build.py rejects a code object with a call.
+// SC: the `_scaled` kernel of the pair (the softmax scale at 0x050 applied in the kernel).
+template <int NT, bool SC>
+__device__ __forceinline__ void full_kernel(uint32_t lds) {
 #ifdef FMHA_TRACE
     const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();
-    Prm p = prm_from_kernarg();
+    Prm p = prm_from_kernarg<SC>();
     p.t_entry = t_entry;
 #else
-    const Prm p = prm_from_kernarg();
+    const Prm p = prm_from_kernarg<SC>();
 #endif
     uint32_t qt, head, z;
     block_coords(p.S, p.H, NT / 2, qt, head, z);
     const bool lut = (p.SK + 127u) / 128u < 4u;   // state.rs:75-77
     if (NT == 512) {
         if (p.vs32) {
-            if (lut) attend_pingpong<true, false, true>(p, lds, qt, head, z, 0, 0, p.SK);
-            else attend_pingpong<false, false, true>(p, lds, qt, head, z, 0, 0, p.SK);
+            if (lut) attend_pingpong<true, false, true, false, SC>(p, lds, qt, head, z, 0, 0, p.SK);
+            else attend_pingpong<false, false, true, false, SC>(p, lds, qt, head, z, 0, 0, p.SK);
         } else {
-            if (lut) attend_pingpong<true, false, false>(p, lds, qt, head, z, 0, 0, p.SK);
-            else attend_pingpong<false, false, false>(p, lds, qt, head, z, 0, 0, p.SK);
+            if (lut) attend_pingpong<true, false, false, false, SC>(p, lds, qt, head, z, 0, 0, p.SK);
+            else attend_pingpong<false, false, false, false, SC>(p, lds, qt, head, z, 0, 0, p.SK);
         }
     } else {
         if (p.vs32) {
-            if (lut) attend_pipelined<true, true>(p, lds, qt, head, z, 0, p.SK);
-            else attend_pipelined<false, true>(p, lds, qt, head, z, 0, p.SK);
+            if (lut) attend_pipelined<true, true, SC>(p, lds, qt, head, z, 0, p.SK);
+            else attend_pipelined<false, true, SC>(p, lds, qt, head, z, 0, p.SK);
         } else {
-            if (lut) attend_pipelined<true, false>(p, lds, qt, head, z, 0, p.SK);
-            else attend_pipelined<false, false>(p, lds, qt, head, z, 0, p.SK);
+            if (lut) attend_pipelined<true, false, SC>(p, lds, qt, head, z, 0, p.SK);
+            else attend_pipelined<false, false, SC>(p, lds, qt, head, z, 0, p.SK);
         }
     }
 }
 
-}  // namespace
-
-#define FMHA_LDS_BASE(name)                                                 \
-    __shared__ __attribute__((aligned(1024))) uint8_t name[kLdsBytes]; \
-    const uint32_t name##_base = (uint32_t)(uintptr_t)(LDS_AS uint8_t*)name
-
-extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_vs128(fmha_mxfp8_args a) {
-    FMHA_LDS_BASE(smem);
-    (void)a;   // read through kernarg()
-    full_kernel<512>(smem_base);
-}
-
-extern "C" __global__ void __launch_bounds__(256, 1) fmha_fwd_hd128_mxfp8_v3_t128(fmha_mxfp8_args a) {
-    FMHA_LDS_BASE(smem);
-    (void)a;
-    full_kernel<256>(smem_base);
-}
-
-extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvsplit(fmha_mxfp8_kvsplit_args ka_) {
-    FMHA_LDS_BASE(smem);
-    (void)ka_;   // read through ka<>(); bytes 0x000..0x26F are the base layout
-    Prm p = prm_from_kernarg();
+// The KV-split kernel body (SC as in full_kernel).
+template <bool SC>
+__device__ __forceinline__ void kvsplit_kernel(uint32_t smem_base) {
+    Prm p = prm_from_kernarg<SC>();
     p.flags = 0;   // 0x280 holds the split count in this layout
     p.lse_out = nullptr;
     p.ohat = (uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_kvsplit_args, ptr_ohat));
@@ -1247,14 +1277,59 @@ extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvs
     // order)
     const bool hv = !lut && p.S - qt * 256u <= 128u;
     if (p.vs32) {
-        if (lut) attend_pingpong<true, true, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
-        else if (hv) attend_pingpong<false, true, true, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
-        else attend_pingpong<false, true, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+        if (lut) attend_pingpong<true, true, true, false, SC>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+        else if (hv) attend_pingpong<false, true, true, true, SC>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+        else attend_pingpong<false, true, true, false, SC>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
     } else {
-        if (lut) attend_pingpong<true, true, false>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
-        else if (hv) attend_pingpong<false, true, false, true>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
-        else attend_pingpong<false, true, false>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+        if (lut) attend_pingpong<true, true, false, false, SC>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+        else if (hv) attend_pingpong<false, true, false, true, SC>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
+        else attend_pingpong<false, true, false, false, SC>(p, smem_base, qt, head, bidx, split, key_lo, key_hi);
     }
+}
+
+}  // namespace
+
+#define FMHA_LDS_BASE(name)                                                 \
+    __shared__ __attribute__((aligned(1024))) uint8_t name[kLdsBytes]; \
+    const uint32_t name##_base = (uint32_t)(uintptr_t)(LDS_AS uint8_t*)name
+
+extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_vs128(fmha_mxfp8_args a) {
+    FMHA_LDS_BASE(smem);
+    (void)a;   // read through kernarg()
+    full_kernel<512, false>(smem_base);
+}
+
+extern "C" __global__ void __launch_bounds__(256, 1) fmha_fwd_hd128_mxfp8_v3_t128(fmha_mxfp8_args a) {
+    FMHA_LDS_BASE(smem);
+    (void)a;
+    full_kernel<256, false>(smem_base);
+}
+
+extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvsplit(fmha_mxfp8_kvsplit_args ka_) {
+    FMHA_LDS_BASE(smem);
+    (void)ka_;   // read through ka<>(); bytes 0x000..0x26F are the base layout
+    kvsplit_kernel<false>(smem_base);
+}
+
+// Extension kernels (no counterpart in the reference): the same ABIs, the softmax scale at 0x050 applied in the kernel.
+// The host launches them when FMHA_FLAG_SCALE (0x280 of the full-sequence layout) or FMHA_KVS_SCALE (the split
+// field) is set; the reference-named kernels ignore 0x050, as the reference's do.
+extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_vs128_scaled(fmha_mxfp8_args a) {
+    FMHA_LDS_BASE(smem);
+    (void)a;
+    full_kernel<512, true>(smem_base);
+}
+
+extern "C" __global__ void __launch_bounds__(256, 1) fmha_fwd_hd128_mxfp8_v3_t128_scaled(fmha_mxfp8_args a) {
+    FMHA_LDS_BASE(smem);
+    (void)a;
+    full_kernel<256, true>(smem_base);
+}
+
+extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvsplit_scaled(fmha_mxfp8_kvsplit_args ka_) {
+    FMHA_LDS_BASE(smem);
+    (void)ka_;
+    kvsplit_kernel<true>(smem_base);
 }
 
 // epilogue.rs:89-167 / io.rs:164-185: thread t -> 8 consecutive outputs of row t >> 4 (tail threads redo the last group)

@@ -27,7 +27,8 @@ FMHA_ERR_PATH, FMHA_ERR_WORKSPACE, FMHA_ERR_HIP, FMHA_ERR_NO_DEVICE = 6, 7, 8, 9
 PATH_VS128, PATH_T128, PATH_KVSPLIT = 0, 1, 2
 KVS_F32_PARTIALS = 0x10000   # include/fmha_mxfp8.h FMHA_KVS_F32_PARTIALS
 KVS_V_SEQ32 = 0x20000        # FMHA_KVS_V_SEQ32
-FLAG_CAUSAL, FLAG_V_SEQ32 = 0x1, 0x2   # FMHA_FLAG_*
+KVS_SCALE = 0x40000          # FMHA_KVS_SCALE
+FLAG_CAUSAL, FLAG_V_SEQ32, FLAG_SCALE = 0x1, 0x2, 0x4   # FMHA_FLAG_*
 PATH_NAMES = {PATH_VS128: "vs128", PATH_T128: "t128", PATH_KVSPLIT: "kvsplit"}
 PATH_IDS = {v: k for k, v in PATH_NAMES.items()}
 
@@ -78,7 +79,7 @@ class Params(ctypes.Structure):
                 ("bytes_q_descale", _u64), ("bytes_k_descale", _u64), ("bytes_v_descale", _u64),
                 ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("HK", ctypes.c_int32), ("S", ctypes.c_int32), ("SK", ctypes.c_int32),
                 ("path", ctypes.c_int32), ("splits", ctypes.c_int32), ("causal", ctypes.c_int32),
-                ("f32_partials", ctypes.c_int32), ("v_seq32", ctypes.c_int32)]
+                ("f32_partials", ctypes.c_int32), ("v_seq32", ctypes.c_int32), ("softmax_scale", ctypes.c_float)]
 
 
 assert ctypes.sizeof(Args) == 656 and ctypes.sizeof(KvsplitArgs) == 648 and ctypes.sizeof(CombineArgs) == 36

@@ -53,7 +53,7 @@ def _ws(device, stream, nbytes):
 
 
 def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", splits=None, stream=None, lse=None, causal=False,
-                   partials="fp16"):
+                   partials="fp16", softmax_scale=None):
     """MXFP8 attention forward, head dim 128 (``out = softmax(q k^T) v`` in base 2 with the E8M0 1x32 scales).
 
     q        [B, S, H, 128]   fp8 e4m3 (uint8 or float8_e4m3fn)   k, v [B, SK, HK, 128] (H = gqa HK, gqa a power of two <= 16)
@@ -65,7 +65,9 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     path: "auto" | "vs128" | "t128" | "kvsplit" (``splits`` in {2, 4, 8}). Returns (path, splits).
     Extensions (not in the reference): ``lse`` [B, H, S] f32 receives the natural-log LSE (vs128 / t128);
     ``causal`` applies the bottom-right causal mask (key t visible to query i iff t <= i + SK - S);
-    ``partials="fp32"`` keeps the KV split's partial rows in f32 instead of the reference's fp16.
+    ``partials="fp32"`` keeps the KV split's partial rows in f32 instead of the reference's fp16;
+    ``softmax_scale`` applies the scale in the kernel (``out = softmax(scale q k^T) v`` in natural log): q must then
+    be quantised without it. Default None: the reference's convention (the caller folds scale log2(e) into q).
     """
     if partials not in ("fp16", "fp32"):
         raise ValueError(f"fmha_fwd_mxfp8: partials must be 'fp16' or 'fp32', got {partials!r}")
@@ -108,6 +110,10 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     p.path, p.splits, p.causal = path_id, nsplit, int(bool(causal))
     p.f32_partials = int(partials == "fp32")
     p.v_seq32 = int(v_seq32)
+    if softmax_scale is not None:
+        if not float(softmax_scale) > 0.0:
+            raise ValueError(f"fmha_fwd_mxfp8: softmax_scale must be positive, got {softmax_scale!r}")
+        p.softmax_scale = float(softmax_scale)
     # the workspace only matters for the KV split; size it for the split the dispatch will choose
     want_path, want_splits = (select_path(B, H, S, SK) if path_id < 0 else (path, nsplit))
     ws, ws_bytes = None, 0
@@ -187,15 +193,16 @@ LOG2E_OVER_SQRT_D = 1.4426950408889634 / math.sqrt(D)
 
 
 def fmha_fwd_bf16_via_mxfp8(q, k, v, out=None, *, softmax_scale=None, causal=False, path="auto", splits=None, lse=None, stream=None,
-                            v_scales="tensor"):
+                            v_scales="tensor", scale_in_kernel=False):
     """Attention from bf16 q [B, S, H, 128], k / v [B, SK, HK, 128]: quantises on the GPU (Q scaled by
     softmax_scale * log2(e) before quantisation, default 1/sqrt(128), as ref_host.cpp:238 folds it), then runs
     ``fmha_fwd_mxfp8``. Returns out (bf16 [B, S, H, 128]); ``lse``, when given, receives the natural-log LSE of
     the scaled scores. ``v_scales``: "tensor" (one f32 descale, the reference's) or "seq32" (extension: one E8M0 per
-    32 keys per column)."""
+    32 keys per column). ``scale_in_kernel`` (extension): Q is quantised as it is and the kernel applies the scale."""
     B, S, H, _ = q.shape
     _, SK, HK, _ = k.shape
-    mul = LOG2E_OVER_SQRT_D if softmax_scale is None else 1.4426950408889634 * float(softmax_scale)
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    mul = 1.0 if scale_in_kernel else (LOG2E_OVER_SQRT_D if softmax_scale is None else 1.4426950408889634 * scale)
     qs = alloc_scales(B, S, H, q.device)
     ks = alloc_scales(B, SK, HK, k.device)
     q8 = quantize_mxfp8(q, qs, mul=mul, stream=stream)
@@ -208,7 +215,8 @@ def fmha_fwd_bf16_via_mxfp8(q, k, v, out=None, *, softmax_scale=None, causal=Fal
         raise ValueError(f"v_scales must be 'tensor' or 'seq32', got {v_scales!r}")
     if out is None:
         out = torch.empty(B, S, H, D, dtype=torch.bfloat16, device=q.device)
-    fmha_fwd_mxfp8(q8, k8, v8, qs, ks, vs, out, path=path, splits=splits, stream=stream, lse=lse, causal=causal)
+    fmha_fwd_mxfp8(q8, k8, v8, qs, ks, vs, out, path=path, splits=splits, stream=stream, lse=lse, causal=causal,
+                   softmax_scale=scale if scale_in_kernel else None)
     return out
 
 

@@ -99,7 +99,7 @@ typedef struct fmha_mxfp8_args {
     uint8_t _pad25[12];
     uint32_t s_descale_k_Hs;  /* 0x260 4 */
     uint8_t _pad26[28];
-    uint32_t flags;           /* 0x280 extension flags, 0 = reference semantics: FMHA_FLAG_CAUSAL, FMHA_FLAG_V_SEQ32 */
+    uint32_t flags;           /* 0x280 extension flags, 0 = reference semantics: FMHA_FLAG_CAUSAL, FMHA_FLAG_V_SEQ32, FMHA_FLAG_SCALE */
     uint8_t abi_tail[12];     /* 0x284 */
 } fmha_mxfp8_args;
 
@@ -137,11 +137,18 @@ typedef struct fmha_mxfp8_combine_args {
 /* Extensions of the full-sequence kernels' `flags` (0x280), no counterpart in the reference's MX kernels:
  *   FMHA_FLAG_CAUSAL    the bottom-right causal mask: key t visible to query i iff t <= i + SK - S;
  *   FMHA_FLAG_V_SEQ32   per-32-key V scales: ptr_v_descale (0x220) points to E8M0 bytes [B, ceil(SK/32), HK, 128]
- *                       (one per 32 keys per column, the layout of fmha_mxfp8_quantize_seq32) instead of one f32.
- * For the KV split, FMHA_KVS_V_SEQ32 is OR-ed into kvs_splits (0x280) with the same meaning. */
+ *                       (one per 32 keys per column, the layout of fmha_mxfp8_quantize_seq32) instead of one f32;
+ *   FMHA_FLAG_SCALE     the softmax scale at 0x050 (f32, which the reference's MX kernels ignore: block3.rs:160) is
+ *                       applied in the kernel: the scores are scale q.k (natural-log softmax), i.e. base-2 scores
+ *                       c q.k with c = f32(scale log2 e), so Q must NOT carry the scale (quantise it with mul 1).
+ *                       c = 2^e m (m in [1, 2)): 2^e joins the Q E8M0 exponents and S is multiplied by m
+ *                       (the fp8pt family's way, block3.rs:160-173). c must be a positive normal f32.
+ * For the KV split, FMHA_KVS_V_SEQ32 and FMHA_KVS_SCALE are OR-ed into kvs_splits (0x280) with the same meanings. */
 #define FMHA_FLAG_CAUSAL 0x1u
 #define FMHA_FLAG_V_SEQ32 0x2u
+#define FMHA_FLAG_SCALE 0x4u
 #define FMHA_KVS_V_SEQ32 0x20000u
+#define FMHA_KVS_SCALE 0x40000u
 
 /* Byte sizes of the caller's allocations, checked by the validate calls
  * (the reference's BufferSizes, ..._vs128_abi.h:131-139). */
@@ -230,6 +237,8 @@ typedef struct fmha_mxfp8_params {
     int32_t causal;            /* 0 = the reference semantics; 1 = bottom-right causal mask (extension) */
     int32_t f32_partials;      /* KV split only: 0 = fp16 partial rows (the reference's); 1 = f32 (extension) */
     int32_t v_seq32;           /* 0 = v_descale is one f32 (the reference's); 1 = E8M0 per 32 keys per column (extension) */
+    float softmax_scale;       /* 0 = the reference's convention (the scale is folded into Q before quantisation);
+                                  > 0 = applied in the kernel (FMHA_FLAG_SCALE / FMHA_KVS_SCALE, extension) */
 } fmha_mxfp8_params;
 
 /* fmha_fwd_hd128_mxfp8_auto: dispatch + validate + launch (+ combine), all on

@@ -27,7 +27,7 @@ class Problem(ctypes.Structure):
     _fields_ = [("B", ctypes.c_int), ("H", ctypes.c_int), ("HK", ctypes.c_int), ("S", ctypes.c_int), ("SK", ctypes.c_int),
                 ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
                 ("qs", ctypes.c_void_p), ("ks", ctypes.c_void_p), ("vdescale", ctypes.c_float), ("causal", ctypes.c_int),
-                ("vs32", ctypes.c_void_p)]
+                ("vs32", ctypes.c_void_p), ("qk_scale", ctypes.c_float)]
 
 
 class CheckResult(ctypes.Structure):
@@ -100,9 +100,12 @@ MODES = {"lcg": 0, "uniform": 1, "normal": 2}
 class Inputs:
     """Seeded MXFP8 inputs in the reference layout (ref_host.cpp:183-263), host numpy arrays."""
 
-    def __init__(self, B, H, S, SK, HK=None, mode="normal", seed_mix=0, causal=False, v_seq32=False):
+    def __init__(self, B, H, S, SK, HK=None, mode="normal", seed_mix=0, causal=False, v_seq32=False, qk_scale=0.0):
         HK = HK or H
         self.B, self.H, self.HK, self.S, self.SK, self.causal = B, H, HK, S, SK, bool(causal)
+        # extension: > 0 = the softmax scale applied in the kernel (scores c q.k, c = f32(qk_scale log2 e)); the
+        # generator's Q is used as it is
+        self.qk_scale = float(qk_scale)
         L = lib()
         self.q = np.zeros(B * S * H * D, np.uint8)
         self.k = np.zeros(B * SK * HK * D, np.uint8)
@@ -126,7 +129,7 @@ class Inputs:
     def problem(self):
         p = Problem(self.B, self.H, self.HK, self.S, self.SK, _ptr(self.q).value, _ptr(self.k).value, _ptr(self.v).value,
                     _ptr(self.qs).value, _ptr(self.ks).value, self.vdescale, int(self.causal),
-                    _ptr(self.vs32).value if self.vs32 is not None else None)
+                    _ptr(self.vs32).value if self.vs32 is not None else None, self.qk_scale)
         return p
 
     @property

@@ -37,6 +37,25 @@ static inline double v_block_scale(const mxo_problem* p, int b, int key, int kvh
 /* the per-tensor V descale the output is multiplied by (1 under per-32 V scales) */
 static inline float v_tensor_descale(const mxo_problem* p) { return p->vs32 ? 1.0f : p->vdescale; }
 
+/* The in-kernel softmax scale (extension, qk_scale > 0): c = f32(qk_scale * log2 e) = 2^e m with m in [1, 2). The
+ * kernel adds e to the Q scale exponents (exact) and multiplies S by m; the seed of S is b / m, so that
+ * m (S + b / m) carries the bias. Without the extension c = 1 (e = 0, m = 1). */
+typedef struct { float c, m, rm; int e; } qk_scaling;
+static qk_scaling qk_scaling_of(const mxo_problem* p) {
+    qk_scaling r = {1.0f, 1.0f, 1.0f, 0};
+    if (!(p->qk_scale > 0.0f)) return r;
+    r.c = p->qk_scale * 1.44269504088896340736f;
+    uint32_t u;
+    memcpy(&u, &r.c, 4);
+    r.e = (int)((u >> 23) & 0xffu) - 127;
+    u = (u & 0x007fffffu) | (127u << 23);
+    memcpy(&r.m, &u, 4);
+    r.rm = 1.0f / r.m;
+    return r;
+}
+/* natural-log score multiplier of the fp64 check: ln 2 per base-2 unit, times c */
+static double score_mul(const mxo_problem* p) { return 0.6931471805599453 * (double)qk_scaling_of(p).c; }
+
 /* ------------------------------------------------------------------ scalars */
 
 double mxo_e4m3_decode(uint8_t b) {
@@ -323,7 +342,7 @@ static void check_item(const void* vctx, long item) {
     const mxo_problem* p = c->p;
     const int b = (int)(item / p->H), h = (int)(item % p->H);
     const int gqa = p->H / p->HK, kvh = h / gqa;
-    const double cpu_scale = 0.6931471805599453;
+    const double cpu_scale = score_mul(p);
     double* sc = (double*)malloc(sizeof(double) * (size_t)p->SK);
     double qd[D];
     double worst = 0, sum_abs = 0, max_ref = 0;
@@ -391,6 +410,7 @@ typedef struct {
     int rows;
     int rows_per_item;
     long items_per_bh;
+    float c;           /* base-2 score multiplier (1, or the in-kernel scale's c) */
 } attn_ctx;
 
 static void attn_item(const void* vctx, long item) {
@@ -415,7 +435,7 @@ static void attn_item(const void* vctx, long item) {
             const float* kr = kbase + (size_t)t * kstride;
             float s = 0.0f;
             for (int d = 0; d < D; ++d) s += qr[d] * kr[d];
-            sc[t] = s;
+            sc[t] = s * c->c;
             mx = s > mx ? s : mx;
         }
         float den = 0.0f;
@@ -449,7 +469,7 @@ double mxo_attention_fp32(const mxo_problem* p, int rows, float* out_f32, int th
     }
     struct timespec t0, t1;
     clock_gettime(CLOCK_MONOTONIC, &t0);
-    attn_ctx c = {p, qf, kf, vf, out_f32, rows, 16, 0};
+    attn_ctx c = {p, qf, kf, vf, out_f32, rows, 16, 0, qk_scaling_of(p).c};
     c.items_per_bh = (rows + c.rows_per_item - 1) / c.rows_per_item;
     run_parallel(threads, (long)p->B * p->H * c.items_per_bh, &c, attn_item);
     clock_gettime(CLOCK_MONOTONIC, &t1);
@@ -506,8 +526,9 @@ static void emulate_row(const mxo_problem* p, const recipe_t* rc, int b, int kvh
     for (int d = 0; d < D; ++d) st->o[d] = 0.0f;
     float s[128];
     uint8_t pb[128];
+    const qk_scaling qc = qk_scaling_of(p);
     for (int t0 = klo; t0 < khi; t0 += 128) {
-        const float bb = bias_value(st->w);
+        const float bb = bias_value(st->w) * qc.rm;   /* the seed (b / m; b when unscaled) */
         /* S' = b + S * 2^-9: the scaled QK MFMA of d 0..63 then d 64..127 accumulating onto the reference */
         double qsd[D];
         for (int d = 0; d < D; ++d) qsd[d] = qv[d] * ldexp(1.0, (sq[d / 32] & 0xff) - 127);
@@ -526,7 +547,7 @@ static void emulate_row(const mxo_problem* p, const recipe_t* rc, int b, int kvh
                 }
                 acc = (float)((double)acc + dot);
             }
-            s[j] = acc;
+            s[j] = acc * qc.m;
         }
         const int vlim = khi < kvis ? khi : kvis;
         /* row max over the valid keys (reduce.rs:52-64; masked keys -1e30, reduce.rs:13-49) */
@@ -624,7 +645,8 @@ static void emu_item(const void* vctx, long item) {
     double qv[D];
     int sq[4];
     for (int d = 0; d < D; ++d) qv[d] = mxo_e4m3_decode(p->q[(((size_t)b * p->S + i) * p->H + h) * D + d]);
-    for (int blk = 0; blk < 4; ++blk) sq[blk] = ((int)p->qs[(((size_t)b * p->S + i) * p->H + h) * 4 + blk] - 9) & 0xff;
+    const int qe = qk_scaling_of(p).e;
+    for (int blk = 0; blk < 4; ++blk) sq[blk] = ((int)p->qs[(((size_t)b * p->S + i) * p->H + h) * 4 + blk] - 9 + qe) & 0xff;
     const int kvis = visible_keys(p, i);
     const float vd = v_tensor_descale(p);
     row_state st;

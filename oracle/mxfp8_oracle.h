@@ -42,6 +42,8 @@ typedef struct mxo_problem {
     int causal;         /* bottom-right causal mask: key t visible for query i iff t <= i + SK - S */
     const uint8_t* vs32;/* extension: NULL = one f32 V descale (vdescale, the reference's); else E8M0 V scales
                            [B, ceil(SK/32), HK, 128], one per 32 keys per column, and vdescale is not used */
+    float qk_scale;     /* extension: 0 = the reference's convention (the softmax scale is folded into Q, scores are
+                           base-2 q.k); > 0 = the kernel applies it: base-2 scores c q.k with c = f32(qk_scale log2 e) */
 } mxo_problem;
 
 typedef struct mxo_check_result {

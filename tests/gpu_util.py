@@ -34,7 +34,7 @@ def run(inp, device, path="auto", splits=None, lse=False, poison=True, partials=
         out.view(torch.int16).fill_(0x7fc1)   # NaN: every element must be written
     lse_t = torch.full((inp.B, inp.H, inp.S), float("nan"), dtype=torch.float32, device=device) if lse else None
     used = ops.fmha_fwd_mxfp8(q, k, v, qs, ks, vs, out, path=path, splits=splits, lse=lse_t, causal=inp.causal,
-                              partials=partials)
+                              partials=partials, softmax_scale=inp.qk_scale if inp.qk_scale > 0 else None)
     torch.cuda.synchronize()
     o = out.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
     return o, used, lse_t

@@ -5,6 +5,7 @@ selection, workspace size, argument errors of the auto entry) behaves as the ref
 crates/amdgpu-graph/src/dispatch.rs:494-511). No test here launches a kernel."""
 import ctypes
 import math
+import struct
 import os
 import re
 
@@ -156,7 +157,7 @@ def test_validate_f32_partials_flag():
     ka, sz, g = _kvsplit()
     ka.kvs_splits = 8 | lib.KVS_F32_PARTIALS
     assert lib.validate("kvsplit", ka, sz, g, B=1, HK=8, KL=0) == (0, "")
-    ka.kvs_splits = 8 | (1 << 18)
+    ka.kvs_splits = 8 | (1 << 19)
     rc, msg = lib.validate("kvsplit", ka, sz, g, B=1, HK=8)
     assert rc == lib.FMHA_ERR_KA_RANGE and "0x280" in msg
     ca = lib.CombineArgs(0x1, 0x2, 0x3, 1024, 128, 8 | lib.KVS_F32_PARTIALS)
@@ -181,7 +182,7 @@ def test_validate_v_seq32_flag():
     sz.ptr_v_descale = need
     a.flags = lib.FLAG_V_SEQ32 | lib.FLAG_CAUSAL
     assert lib.validate("vs128", a, sz, grid, HK=HK) == (0, "")
-    a.flags = 0x4
+    a.flags = 0x8
     rc, msg = lib.validate("vs128", a, sz, grid, HK=HK)
     assert rc == lib.FMHA_ERR_KA_RANGE and "0x280" in msg
     ka, ksz, g = _kvsplit(B=1, H=8, HK=8, S=128, SK=16384, splits=8)
@@ -269,3 +270,46 @@ def test_init_without_gpu_reports_error():
     err = ctypes.create_string_buffer(256)
     rc = lib.raw.fmha_mxfp8_init(err, 256)
     assert rc in (lib.FMHA_ERR_NO_DEVICE, lib.FMHA_ERR_HIP) and err.value
+
+
+def _f32_bits(x):
+    return struct.unpack("<I", struct.pack("<f", x))[0]
+
+
+def test_validate_scale_flag():
+    """The in-kernel softmax scale (extension, flags bit 2 / kvs_splits bit 18) reads the f32 at 0x050, which the
+    reference's MX kernels ignore: c = scale log2(e) must be a positive normal f32. Without the flag 0x050 is not
+    checked (the reference's hosts write 1/sqrt(128) there)."""
+    B, H, HK, S, SK = 2, 8, 4, 300, 1000
+    a, sz = _shape_args(B, H, HK, S, SK)
+    grid = (math.ceil(S / 256), H, B)
+    a.softmax_scale = _f32_bits(float("nan"))
+    assert lib.validate("vs128", a, sz, grid, HK=HK) == (0, "")
+    a.flags = lib.FLAG_SCALE
+    for bad in (0.0, -0.125, float("inf"), float("nan"), 1e-39, 3e38):
+        a.softmax_scale = _f32_bits(bad)
+        rc, msg = lib.validate("vs128", a, sz, grid, HK=HK)
+        assert rc == lib.FMHA_ERR_KA_RANGE and "0x50" in msg, (bad, rc, msg)
+    for good in (0.08838834764831845, 1.0, 2.0 ** -20, 1e4):
+        a.softmax_scale = _f32_bits(good)
+        assert lib.validate("vs128", a, sz, grid, HK=HK) == (0, ""), good
+        assert lib.validate("t128", a, sz, (math.ceil(S / 128), H, B), HK=HK) == (0, ""), good
+    ka, ksz, g = _kvsplit()
+    set_scale = lambda x: ctypes.memmove(ctypes.addressof(ka) + 0x50, struct.pack("<f", x), 4)   # the base layout is raw bytes
+    set_scale(0.0)
+    assert lib.validate("kvsplit", ka, ksz, g, B=1, HK=8, KL=0) == (0, "")
+    ka.kvs_splits = 8 | lib.KVS_SCALE
+    assert lib.validate("kvsplit", ka, ksz, g, B=1, HK=8)[0] == lib.FMHA_ERR_KA_RANGE
+    set_scale(0.5)
+    assert lib.validate("kvsplit", ka, ksz, g, B=1, HK=8, KL=0) == (0, "")
+
+
+def test_code_objects_have_no_calls():
+    """Every kernel is one function: an outlined callee gets no kernel-argument pointer (it is not an ABI input) and
+    reads its arguments from address 0. A code object with a call must not exist (build.py refuses to produce one)."""
+    from amdgpu_rustdsl_amd import build
+    for name in ("fmha_mxfp8_gfx950.hsaco", "mxfp8_quant_gfx950.hsaco"):
+        path = os.path.join(os.path.dirname(lib.LIB_PATH), name)
+        if not os.path.exists(path):
+            pytest.skip(f"{name} not built")
+        assert build.code_object_calls(path) == [], name

@@ -219,3 +219,38 @@ def test_parity_split_tiles(gpu, case):
     assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"]
     assert cmp["mean_abs"] <= 0.6 * ref_stats["mean_err"], cmp
     assert cmp["max_abs"] <= 0.05, cmp
+
+
+# Extension: the softmax scale applied in the kernel (kernarg 0x050 with FMHA_FLAG_SCALE / FMHA_KVS_SCALE): Q is the
+# generator's, the scores become c q.k with c = f32(scale log2 e) = 2^e m, the exponent joining the Q scales and S
+# multiplied by m. Bar: the statistical one against the oracle's emulation of the same arithmetic, on every path.
+QK_SCALE_CASES = [
+    ("vs128_B2H8S1024_c1", 2, 8, 8, 1024, 1024, False, False, "vs128", None, 0.6931471805599453),
+    ("vs128_ragged_S700_SK1000_c2.16", 1, 8, 2, 700, 1000, False, False, "vs128", None, 1.5),
+    ("t128_B1H4S512_SK600_c0.43", 1, 4, 4, 512, 600, False, False, "t128", None, 0.3),
+    ("t128_lut_SK100_c1.44", 1, 2, 2, 256, 100, False, False, "t128", None, 1.0),
+    ("kvsplit_S128_SK4096_split4_c0.72", 1, 8, 8, 128, 4096, False, False, "kvsplit", 4, 0.5),
+    ("kvsplit_S300_SK2000_split2_c1.15", 1, 4, 4, 300, 2000, False, False, "kvsplit", 2, 0.8),
+    ("causal_vs128_S1024_c1.3", 1, 8, 8, 1024, 1024, True, False, "vs128", None, 0.9),
+    ("vs32_vs128_S512_SK777_c0.87", 1, 4, 4, 512, 777, False, True, "vs128", None, 0.6),
+]
+
+
+@pytest.mark.parametrize("case", QK_SCALE_CASES, ids=[c[0] for c in QK_SCALE_CASES])
+def test_parity_qk_scale(gpu, case):
+    name, B, H, HK, S, SK, causal, vs32, path, splits, scale = case
+    print(f"[case] qk scale {name}", flush=True)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal, v_seq32=vs32, qk_scale=scale)
+    out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
+    assert used[0] == path
+    used_splits = used[1] if used[0] == "kvsplit" else 0
+    rows = S if path == "kvsplit" else min(S, 256 if causal else ROWS)
+    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows)
+    stats = oracle.check_fp64(inp, out, rows=rows)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
+    print(f"[case] qk scale {name} path={used} ours={stats} emulated={ref_stats} vs-emulation={cmp}", flush=True)
+    assert not np.isnan(oracle.bf16_to_f32(out)).any()
+    assert stats["bad"] <= ref_stats["bad"]
+    assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
+    assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
+    assert cmp["max_abs"] <= 0.05, cmp

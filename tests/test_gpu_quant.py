@@ -228,3 +228,24 @@ def test_fmha_from_bf16_with_v_seq32(gpu):
     print(f"[case] bf16 via mxfp8: seq32 mean {err.mean().item():.3g} max {err.max().item():.3g}; "
           f"tensor mean {err_t.mean().item():.3g}", flush=True)
     assert err.mean().item() < 0.01 and err.max().item() < 0.1
+
+
+@pytest.mark.parametrize("scale", [1.0 / math.sqrt(D), 0.05])
+def test_fmha_from_bf16_scale_in_kernel(gpu, scale):
+    """Extension end to end: Q quantised as it is and the softmax scale applied in the kernel
+    (scale_in_kernel=True) against fp32 attention on the bf16 inputs, within the MXFP8 error bar of the reference's
+    convention (Q quantised with the scale folded in) on the same inputs."""
+    B, H, S, SK = 1, 4, 512, 640
+    g = torch.Generator(device=gpu)
+    g.manual_seed(5)
+    qf, kf, vf = (torch.randn(B, n, H, D, generator=g, device=gpu, dtype=torch.bfloat16) for n in (S, SK, SK))
+    att = torch.softmax(torch.einsum("bshd,bthd->bhst", qf.float(), kf.float()) * scale, dim=-1)
+    exact = torch.einsum("bhst,bthd->bshd", att, vf.float())
+    folded = ops.fmha_fwd_bf16_via_mxfp8(qf, kf, vf, softmax_scale=scale)
+    inkernel = ops.fmha_fwd_bf16_via_mxfp8(qf, kf, vf, softmax_scale=scale, scale_in_kernel=True)
+    torch.cuda.synchronize()
+    e_fold = (folded.float() - exact).abs()
+    e_in = (inkernel.float() - exact).abs()
+    print(f"[case] scale {scale}: folded mean {e_fold.mean().item():.3e} max {e_fold.max().item():.3e}; "
+          f"in kernel mean {e_in.mean().item():.3e} max {e_in.max().item():.3e}", flush=True)
+    assert e_in.mean().item() <= 1.25 * e_fold.mean().item() and e_in.max().item() < 0.1

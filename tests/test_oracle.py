@@ -536,3 +536,48 @@ def test_split_tile_order_accuracy(boost):
     st_stats = oracle.check_fp64(inp, oracle.emulate(inp, splits=4, rows=0, split_tiles=True), rows=S)
     assert st_stats["bad"] <= ref_stats["bad"]
     assert st_stats["mean_err"] <= 1.10 * ref_stats["mean_err"]
+
+
+def _scale_for_c(c_target):
+    """An f32 softmax scale whose f32(scale * log2 e) is exactly c_target (searched among neighbouring f32 values)."""
+    l2e = np.float32(1.4426950408889634)
+    s = np.float32(c_target) / l2e
+    for _ in range(64):
+        c = np.float32(s) * l2e
+        if c == np.float32(c_target):
+            return float(s)
+        s = np.nextafter(s, np.float32(np.inf) if c < c_target else np.float32(0), dtype=np.float32)
+    raise AssertionError("no f32 scale found")
+
+
+@pytest.mark.parametrize("splits", [0, 2])
+def test_qk_scale_power_of_two_is_a_q_exponent_shift(splits):
+    """The in-kernel softmax scale (extension) with c = scale log2 e = 2^-3 exactly (mantissa 1) must give the same bits
+    as the unscaled recipe on Q scales lowered by 3 binades: the exponent goes into the Q E8M0 bytes, nothing else."""
+    B, H, S, SK = 1, 2, 64, 700
+    scaled = oracle.Inputs(B, H, S, SK, qk_scale=_scale_for_c(0.125))
+    shifted = oracle.Inputs(B, H, S, SK)
+    n = B * S * H * 4
+    assert (shifted.qs[:n] >= 3 + 9).all()
+    shifted.qs[:n] -= 3
+    np.testing.assert_array_equal(oracle.emulate(scaled, splits=splits, rows=0), oracle.emulate(shifted, splits=splits, rows=0))
+
+
+@pytest.mark.parametrize("splits", [0, 4])
+def test_qk_scale_mantissa(splits):
+    """c = 1.5 x 2^-3 (mantissa 1.5): the recipe multiplies S by 1.5 after seeding it with b / 1.5. Against fp64
+    attention with scores ln2 c q.k it must stay as accurate as the unscaled recipe (a missing or inverted mantissa
+    multiply changes every score by 1.5x and fails), and the CPU fp32 attention must agree with the fp64 check."""
+    B, H, S, SK = 1, 2, 64, 1500
+    base = oracle.Inputs(B, H, S, SK)
+    ref = oracle.check_fp64(base, oracle.emulate(base, splits=splits, rows=0), rows=S)
+    inp = oracle.Inputs(B, H, S, SK, qk_scale=_scale_for_c(0.1875))
+    got = oracle.check_fp64(inp, oracle.emulate(inp, splits=splits, rows=0), rows=S)
+    assert got["bad"] == 0 and got["mean_err"] <= 2.0 * ref["mean_err"], (got, ref)
+    # the unscaled recipe on the same Q misses the factor 1.5 x 2^-3: far off
+    wrong = oracle.check_fp64(inp, oracle.emulate(base, splits=splits, rows=0), rows=S)
+    assert wrong["mean_err"] > 10 * got["mean_err"]
+    _, f32 = oracle.attention_fp32(inp, rows=S)
+    u = np.ascontiguousarray(f32, dtype=np.float32).view(np.uint32)
+    as_bf16 = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)   # round to nearest even
+    assert oracle.check_fp64(inp, as_bf16, rows=S)["mean_err"] < 0.5 * got["mean_err"]
