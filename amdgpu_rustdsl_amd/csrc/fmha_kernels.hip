@@ -38,6 +38,8 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef short v2s __attribute__((ext_vector_type(2)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 
 #define LDS_AS __attribute__((address_space(3)))
 // wave issue priority around the MFMA phases
@@ -159,7 +161,7 @@ __device__ inline void set_qk_scale(Prm& p, bool on) {
 
 // SC: the `_scaled` kernels, which apply the softmax scale at 0x050; the reference-named kernels fold qk_m = qk_rm = 1,
 // qk_e = 0 as constants (their code carries nothing of the extension).
-template <bool SC = false>
+template <bool SC = false, bool KVS = false>
 __device__ inline Prm prm_from_kernarg() {
     Prm p;
     p.q = (const uint8_t*)KA_FIELD(uint64_t, ptr_q); p.k = (const uint8_t*)KA_FIELD(uint64_t, ptr_k);
@@ -179,7 +181,10 @@ __device__ inline Prm prm_from_kernarg() {
     p.ohat = nullptr; p.lse = nullptr; p.splits = 1; p.rows_total = 0; p.f32_partials = 0;
     set_qk_scale(p, SC);
 #ifdef FMHA_TRACE
-    p.trace = (uint64_t*)(uintptr_t)(ka<uint32_t>(0x288) | ((uint64_t)ka<uint32_t>(0x28C) << 32));
+    // the trace buffer: 0x288 of the 656-byte layout; the KV split's 648-byte layout ends there, so it reads the
+    // unused 0x040 slot instead
+    if (KVS) p.trace = (uint64_t*)(uintptr_t)ka<uint64_t>(0x040);
+    else p.trace = (uint64_t*)(uintptr_t)(ka<uint32_t>(0x288) | ((uint64_t)ka<uint32_t>(0x28C) << 32));
 #endif
     return p;
 }
@@ -871,6 +876,7 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
     } else {
         if (sync) block_barrier();
         const uint32_t sbase = w.lds + kLdsEpi + wave_id() * 32u * kEpiRow;
+        const float fin16 = fin * 0.0625f;   // (x / 16) fin == x (fin / 16) exactly: 1/16 is a power of two
 #pragma unroll
         for (int dc = 0; dc < 4; ++dc)
 #pragma unroll
@@ -883,7 +889,12 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
                         const v2bf b = {(__bf16)(x0 * fin), (__bf16)(x1 * fin)};
                         wd[c] = __builtin_bit_cast(uint32_t, b);
                     } else {
-                        wd[c] = f2h((x0 * 0.0625f) * fin) | (f2h((x1 * 0.0625f) * fin) << 16);
+                        // the f32 products are rounded, then converted to f16 (RNE): the empty asm keeps the compiler
+                        // from fusing product and conversion into one rounding (v_fma_mix), which differs in
+                        // double-rounding cases; v_cvt_pk_f16_f32 converts the pair
+                        float y0 = x0 * fin16, y1 = x1 * fin16;
+                        asm volatile("" : "+v"(y0), "+v"(y1));
+                        wd[c] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){y0, y1}, v2h));
                     }
                 }
                 *(LDS_AS v2i*)(uintptr_t)(sbase + n * kEpiRow + (32 * dc + 8 * a + dbase) * 2) = (v2i){(int)wd[0], (int)wd[1]};
@@ -1252,7 +1263,13 @@ __device__ __forceinline__ void full_kernel(uint32_t lds) {
 // The KV-split kernel body (SC as in full_kernel).
 template <bool SC>
 __device__ __forceinline__ void kvsplit_kernel(uint32_t smem_base) {
-    Prm p = prm_from_kernarg<SC>();
+#ifdef FMHA_TRACE
+    const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();
+    Prm p = prm_from_kernarg<SC, true>();
+    p.t_entry = t_entry;
+#else
+    Prm p = prm_from_kernarg<SC, true>();
+#endif
     p.flags = 0;   // 0x280 holds the split count in this layout
     p.lse_out = nullptr;
     p.ohat = (uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_kvsplit_args, ptr_ohat));
