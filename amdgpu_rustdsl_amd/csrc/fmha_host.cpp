@@ -76,7 +76,7 @@ namespace {
 using fmha_internal::fail;
 using fmha_internal::set_err;
 
-const char* const kKernelNames[7] = {
+const char* const kKernelNames[9] = {
     "fmha_fwd_hd128_mxfp8_v3_vs128",
     "fmha_fwd_hd128_mxfp8_v3_t128",
     "fmha_fwd_hd128_mxfp8_v3_kvsplit",
@@ -85,10 +85,23 @@ const char* const kKernelNames[7] = {
     "fmha_fwd_hd128_mxfp8_v3_vs128_scaled",
     "fmha_fwd_hd128_mxfp8_v3_t128_scaled",
     "fmha_fwd_hd128_mxfp8_v3_kvsplit_scaled",
+    // extension kernels: t128's grid with 512 threads, the two wave groups splitting each tile's keys
+    "fmha_fwd_hd128_mxfp8_v3_t128_split_tiles",
+    "fmha_fwd_hd128_mxfp8_v3_t128_split_tiles_scaled",
 };
-enum { K_VS128 = 0, K_T128 = 1, K_KVSPLIT = 2, K_COMBINE = 3, K_VS128_SC = 4, K_T128_SC = 5, K_KVSPLIT_SC = 6 };
+enum { K_VS128 = 0, K_T128 = 1, K_KVSPLIT = 2, K_COMBINE = 3, K_VS128_SC = 4, K_T128_SC = 5, K_KVSPLIT_SC = 6, K_T128ST = 7,
+       K_T128ST_SC = 8 };
 
-fmha_internal::ModuleCache<7> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
+// t128's shapes run on the split-tile kernel (512 threads) unless the whole sequence has fewer than 4 key tiles (the
+// LUT recipe, state.rs:75-77), which keeps the reference's order on the one-wave-per-SIMD kernel (256 threads)
+bool t128_split_tiles(uint32_t SK) { return (SK + 127u) / 128u >= 4u; }
+int t128_kernel(uint32_t SK, bool scaled, uint32_t* block) {
+    const bool st = t128_split_tiles(SK);
+    *block = st ? 512u : 256u;
+    return st ? (scaled ? K_T128ST_SC : K_T128ST) : (scaled ? K_T128_SC : K_T128);
+}
+
+fmha_internal::ModuleCache<9> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
 
 int get_functions(hipFunction_t** out, char* err, size_t errlen) { return g_fmha.get(out, err, errlen); }
 
@@ -311,7 +324,9 @@ int fmha_mxfp8_launch_vs128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, 
     return launch_raw((a->flags & FMHA_FLAG_SCALE) ? K_VS128_SC : K_VS128, a, sizeof(*a), gx, gy, gz, 512, stream, nullptr, 0);
 }
 int fmha_mxfp8_launch_t128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream) {
-    return launch_raw((a->flags & FMHA_FLAG_SCALE) ? K_T128_SC : K_T128, a, sizeof(*a), gx, gy, gz, 256, stream, nullptr, 0);
+    uint32_t block;
+    const int kern = t128_kernel(a->s_kv_seq_len, (a->flags & FMHA_FLAG_SCALE) != 0, &block);
+    return launch_raw(kern, a, sizeof(*a), gx, gy, gz, block, stream, nullptr, 0);
 }
 int fmha_mxfp8_launch_kvsplit(const fmha_mxfp8_kvsplit_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream) {
     return launch_raw((a->kvs_splits & FMHA_KVS_SCALE) ? K_KVSPLIT_SC : K_KVSPLIT, a, sizeof(*a), gx, gy, gz, 512, stream, nullptr, 0);
@@ -368,8 +383,9 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
         int rc = path == FMHA_PATH_VS128 ? fmha_mxfp8_validate_vs128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen)
                                          : fmha_mxfp8_validate_t128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen);
         if (rc != FMHA_OK) return rc;
-        const int kern = path == FMHA_PATH_VS128 ? (scaled ? K_VS128_SC : K_VS128) : (scaled ? K_T128_SC : K_T128);
-        return launch_raw(kern, &a, sizeof(a), gx, gy, (uint32_t)B, (uint32_t)(rows * 2), stream,
+        uint32_t block = 512u;
+        const int kern = path == FMHA_PATH_VS128 ? (scaled ? K_VS128_SC : K_VS128) : t128_kernel((uint32_t)SK, scaled, &block);
+        return launch_raw(kern, &a, sizeof(a), gx, gy, (uint32_t)B, block, stream,
                           err, errlen);
     }
     // KV split: partials (fp32-sized rows, as ref_host.cpp:149 / ops.py:133) then the LSE, both in the workspace

@@ -563,16 +563,17 @@ struct Wave {
 
     // Lane constants, softmax state, and the loads of the lane's Q bytes and scales. The Q bytes stay in registers
     // (16 VGPRs) for the whole key range: re-reading them from LDS every tile cost 32 KiB of LDS reads per tile and block.
-    // rwave: the wave's 32-row block in the block's rows (its wave index, or wave % 4 when the two groups share rows)
+    // rwave: the wave's 32-row block in the block's rows (its wave index, or wave % 4 when the two groups share rows);
+    // rb: query rows per block (ROWS, or 128 for the full-sequence split-tile kernel)
     __device__ __forceinline__ void init(const Prm& p, uint32_t lds_, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_hi_,
-                                         uint32_t rwave) {
+                                         uint32_t rwave, uint32_t rb = ROWS) {
         lane = threadIdx.x & 63u;
         wave = wave_id();
         n = lane & 31u;
         hh = lane >> 5;
         lds = lds_;
         key_hi = key_hi_;
-        row0 = qtile * ROWS + rwave * 32u;
+        row0 = qtile * rb + rwave * 32u;
         const uint32_t row = row0 + n;
         const uint32_t row_c = min(row, p.S - 1u);
         kfo = n * 128u + ((hh ^ swz(n)) << 4);
@@ -994,12 +995,15 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     if (p.trace && (threadIdx.x & 63u) == 0u) p.trace[((size_t)tblk * 8u + (threadIdx.x >> 6)) * 8u + 7u] = p.t_entry;
 #endif
     Wave<NT> w;
-    w.init(p, lds, qtile, head, bidx, key_hi, HV ? wave_id() & 3u : wave_id());
+    // rows per block: 256, or 128 for the full-sequence split-tile kernel (the KV split's split-tile blocks keep the
+    // 256-row grid and use their first 128 rows)
+    constexpr uint32_t RB = HV && !SPLIT ? 128u : 256u;
+    w.init(p, lds, qtile, head, bidx, key_hi, HV ? wave_id() & 3u : wave_id(), RB);
     FMHA_MARK(p, tblk, 1);
     const uint32_t kvh = head / p.gqa;
     const bool causal = (p.flags & 1u) != 0;
     uint32_t key_end = key_hi;   // the block's last useful key + 1
-    if (causal) key_end = (uint32_t)max(0, min((int)key_hi, (int)(qtile * Wave<NT>::ROWS + Wave<NT>::ROWS - 1) + (int)p.SK - (int)p.S + 1));
+    if (causal) key_end = (uint32_t)max(0, min((int)key_hi, (int)(qtile * RB + RB - 1) + (int)p.SK - (int)p.S + 1));
     const uint32_t ntiles = key_end > key_lo ? (key_end - key_lo + kTile - 1) / kTile : 0;
 
     Stager<NT> st;
@@ -1304,6 +1308,31 @@ __device__ __forceinline__ void kvsplit_kernel(uint32_t smem_base) {
     }
 }
 
+// The full-sequence split-tile kernel (extension): the t128 grid (128 query rows per block) with 512 threads; both wave
+// groups take the block's rows and split each tile's keys (HV), so one group converts while the other multiplies,
+// which one wave per SIMD cannot do. The host launches it for t128's shapes with the non-LUT recipe; the LUT case is
+// served too (the merge is exact either way), for direct launches.
+template <bool SC>
+__device__ __forceinline__ void t128_split_tiles_kernel(uint32_t lds) {
+#ifdef FMHA_TRACE
+    const uint64_t t_entry = __builtin_amdgcn_s_memrealtime();
+    Prm p = prm_from_kernarg<SC>();
+    p.t_entry = t_entry;
+#else
+    const Prm p = prm_from_kernarg<SC>();
+#endif
+    uint32_t qt, head, z;
+    block_coords(p.S, p.H, 128u, qt, head, z);
+    const bool lut = (p.SK + 127u) / 128u < 4u;   // state.rs:75-77
+    if (p.vs32) {
+        if (lut) attend_pingpong<true, false, true, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
+        else attend_pingpong<false, false, true, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
+    } else {
+        if (lut) attend_pingpong<true, false, false, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
+        else attend_pingpong<false, false, false, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
+    }
+}
+
 }  // namespace
 
 #define FMHA_LDS_BASE(name)                                                 \
@@ -1347,6 +1376,19 @@ extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_kvs
     FMHA_LDS_BASE(smem);
     (void)ka_;
     kvsplit_kernel<true>(smem_base);
+}
+
+// Extension kernels (no counterpart in the reference): t128's grid and kernarg layout, 512 threads, split tiles.
+extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_t128_split_tiles(fmha_mxfp8_args a) {
+    FMHA_LDS_BASE(smem);
+    (void)a;
+    t128_split_tiles_kernel<false>(smem_base);
+}
+
+extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_t128_split_tiles_scaled(fmha_mxfp8_args a) {
+    FMHA_LDS_BASE(smem);
+    (void)a;
+    t128_split_tiles_kernel<true>(smem_base);
 }
 
 // epilogue.rs:89-167 / io.rs:164-185: thread t -> 8 consecutive outputs of row t >> 4 (tail threads redo the last group)

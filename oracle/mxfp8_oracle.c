@@ -607,8 +607,8 @@ static void emulate_row(const mxo_problem* p, const recipe_t* rc, int b, int kvh
 }
 
 /* The library's split-tile order (extension, no reference counterpart): a KV-split block with at most 128 query rows
- * (S - 256 floor(i / 256) <= 128) and the non-LUT recipe runs two streams per row, keys 0..63 and 64..127 of every
- * tile, and merges them: with b the stream's bias (O and l carry 2^(512 b)), the smaller b is kept and the other
+ * (S - 256 floor(i / 256) <= 128), and every row of the full-sequence split-tile kernel (the t128 path), with the
+ * non-LUT recipe, run two streams per row, keys 0..63 and 64..127 of every tile, and merge them: with b the stream's bias (O and l carry 2^(512 b)), the smaller b is kept and the other
  * stream scaled by 2^(512 (b_min - b)), O = fma(O_b, s_b, O_a s_a) in the order of the kernel's merge. */
 static int split_tile_order(const mxo_problem* p, const recipe_t* rc, int i) {
     return !rc->lut && p->S - 256 * (i / 256) <= 128;
@@ -652,7 +652,15 @@ static void emu_item(const void* vctx, long item) {
     row_state st;
     uint16_t* orow = c->out + (((size_t)b * p->S + i) * p->H + h) * D;
     if (c->splits <= 0) {
-        emulate_row(p, &rc, b, kvh, qv, sq, 0, p->SK, kvis, 0, 128, &st);
+        if (c->split_tiles && !rc.lut) {
+            /* the full-sequence split-tile kernel (t128's shapes): every row in the two-stream order */
+            row_state st_b;
+            emulate_row(p, &rc, b, kvh, qv, sq, 0, p->SK, kvis, 0, 64, &st);
+            emulate_row(p, &rc, b, kvh, qv, sq, 0, p->SK, kvis, 64, 128, &st_b);
+            merge_streams(&st, &st_b);
+        } else {
+            emulate_row(p, &rc, b, kvh, qv, sq, 0, p->SK, kvis, 0, 128, &st);
+        }
         /* state.rs:79-83 (v_rcp_f32, then x v_descale); a row with no visible key (causal extension, S > SK) is 0 */
         const float fin = st.l > 0.0f ? (1.0f / st.l) * vd : 0.0f;
         for (int d = 0; d < D; ++d) orow[d] = mxo_f32_to_bf16(st.o[d] * fin);

@@ -113,7 +113,8 @@ void mxo_combine(const uint16_t* ohat_f16, const float* lse, uint16_t* out_bf16,
 
 /* Extension (no reference counterpart): mxo_emulate with the KV split's partial rows kept in f32 when f32_partials
  * (ohat then receives f32 rows), and the combine on f32 partial rows. split_tiles: the library's split-tile order
- * for KV-split blocks of at most 128 query rows (two 64-key streams per tile, merged; non-LUT recipe only).
+ * (two 64-key streams per tile, merged; non-LUT recipe only) for KV-split blocks of at most 128 query rows, and,
+ * with splits = 0, for every row (the t128 path's split-tile kernel).
  * mxo_emulate is mxo_emulate_ex(..., 0, 0, ...). */
 void mxo_emulate_ex(const mxo_problem* p, int splits, int rows, uint16_t* out_bf16, void* ohat, float* lse_f32,
                     int f32_partials, int split_tiles, int threads);

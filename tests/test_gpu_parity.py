@@ -37,12 +37,13 @@ CASES = [
 ]
 
 
-def _emulated_bar(inp, splits, rows=ROWS, **kw):
+def _emulated_bar(inp, splits, rows=ROWS, path=None, **kw):
     """The reference's error statistics (its order), and the emulation to compare element-wise with: the library's
-    own order, which differs from the reference's for KV-split blocks of at most 128 query rows (split tiles)."""
+    own order, which differs from the reference's for KV-split blocks of at most 128 query rows and on the t128 path
+    (split tiles; not with the LUT recipe, which the emulation handles)."""
     emu = oracle.emulate(inp, splits=splits, rows=rows, **kw)
     ref_stats = oracle.check_fp64(inp, emu, rows=rows)
-    if splits:
+    if splits or path == "t128":
         emu = oracle.emulate(inp, splits=splits, rows=rows, split_tiles=True, **kw)
     return emu, ref_stats
 
@@ -54,7 +55,7 @@ def test_parity(gpu, case):
     inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
     out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
     used_splits = used[1] if used[0] == "kvsplit" else 0
-    emu, ref_stats = _emulated_bar(inp, used_splits)
+    emu, ref_stats = _emulated_bar(inp, used_splits, path=used[0])
     stats = oracle.check_fp64(inp, out, rows=ROWS)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, min(ROWS, S))
     print(f"[case] {name} path={used} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
@@ -88,8 +89,7 @@ def test_parity_causal(gpu, case):
     # rows checked: all of them for the small shapes, the first 256 of every (b, h) for cfg4 (its first block,
     # whose keys are cut by the mask on every tile of the diagonal)
     rows = S if B * H * S * SK <= (1 << 24) else 256
-    emu = oracle.emulate(inp, rows=rows)
-    ref_stats = oracle.check_fp64(inp, emu, rows=rows)
+    emu, ref_stats = _emulated_bar(inp, 0, rows=rows, path=used[0])
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
     print(f"[case] {name} path={used} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
@@ -154,7 +154,7 @@ def test_parity_v_seq32(gpu, case):
     assert used[0] == path
     used_splits = used[1] if used[0] == "kvsplit" else 0
     rows = min(S, 256 if causal else ROWS)
-    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows)
+    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0])
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
     print(f"[case] v_seq32 {name} path={used} ours={stats} emulated={ref_stats} vs-emulation={cmp}", flush=True)
@@ -245,7 +245,7 @@ def test_parity_qk_scale(gpu, case):
     assert used[0] == path
     used_splits = used[1] if used[0] == "kvsplit" else 0
     rows = S if path == "kvsplit" else min(S, 256 if causal else ROWS)
-    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows)
+    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0])
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
     print(f"[case] qk scale {name} path={used} ours={stats} emulated={ref_stats} vs-emulation={cmp}", flush=True)
@@ -254,3 +254,46 @@ def test_parity_qk_scale(gpu, case):
     assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
     assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
     assert cmp["max_abs"] <= 0.05, cmp
+
+
+# The t128 path's split-tile kernel (extension: 512 threads on t128's 128-row blocks, the two wave groups splitting each
+# tile's keys), on every row: shapes of the reference's t128 dispatch, GQA, a ragged tail, causal, and through the
+# direct launcher (fmha_mxfp8_launch_t128 uses the same kernel).
+T128_ST_CASES = [
+    ("B1H8S1024", 1, 8, 8, 1024, 1024, False),
+    ("B2H8S512_gqa4", 2, 8, 2, 512, 512, False),
+    ("B1H8S1000_SK1337", 1, 8, 8, 1000, 1337, False),
+    ("B1H4S700_SK700_causal", 1, 4, 4, 700, 700, True),
+    ("B1H2S100_SK2000", 1, 2, 2, 100, 2000, False),
+]
+
+
+@pytest.mark.parametrize("case", T128_ST_CASES, ids=[c[0] for c in T128_ST_CASES])
+def test_parity_t128_split_tiles(gpu, case):
+    name, B, H, HK, S, SK, causal = case
+    print(f"[case] t128 split tiles {name}", flush=True)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
+    out, used, _ = gpu_util.run(inp, gpu, path="t128")
+    assert used[0] == "t128"
+    emu, ref_stats = _emulated_bar(inp, 0, rows=S, path="t128")
+    stats = oracle.check_fp64(inp, out, rows=S)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, S)
+    print(f"[case] t128 split tiles {name} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
+    assert not np.isnan(oracle.bf16_to_f32(out)).any()
+    assert stats["bad"] <= ref_stats["bad"]
+    assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
+    assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
+    assert cmp["max_abs"] <= 0.05, cmp
+    if not causal:
+        # the direct launcher picks the same kernel (512 threads, t128's grid): bit-identical output
+        import ctypes, math, torch
+        from amdgpu_rustdsl_amd import lib
+        q, k, v, qs, ks, vs = gpu_util.upload(inp, gpu)
+        o2 = torch.full((B, S, H, 128), float("nan"), dtype=torch.bfloat16, device=gpu)
+        a = lib.fill_args(o2.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), qs.data_ptr(), ks.data_ptr(), vs.data_ptr(),
+                          B, H, HK, S, SK)
+        st = torch.cuda.current_stream(gpu).cuda_stream
+        assert lib.raw.fmha_mxfp8_launch_t128(ctypes.byref(a), math.ceil(S / 128), H, B, st) == 0
+        torch.cuda.synchronize()
+        direct = o2.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+        np.testing.assert_array_equal(direct, out)

@@ -493,13 +493,28 @@ def test_quant_seq32_is_rows_rule_on_transposed_blocks(B, SK, HK):
 def test_split_tile_order_rule():
     """The split-tile order (extension: the library's KV split on blocks of at most 128 query rows) changes only the
     rows of such blocks: with S = 300 the rows of block 0 (300 valid rows) are bit-identical to the reference's order,
-    rows 256..299 (44 valid rows) are not; full-sequence emulation ignores the flag."""
+    rows 256..299 (44 valid rows) are not. Full-sequence emulation (the t128 path's split-tile kernel) takes every row
+    in the split-tile order, except with the LUT recipe (fewer than 4 key tiles), which keeps the reference's."""
     inp = oracle.Inputs(1, 2, 300, 1000)
     ref = oracle.emulate(inp, splits=2, rows=0).reshape(1, 300, 2, D)
     st = oracle.emulate(inp, splits=2, rows=0, split_tiles=True).reshape(ref.shape)
     np.testing.assert_array_equal(st[:, :256], ref[:, :256])
     assert (st[:, 256:] != ref[:, 256:]).any()
-    np.testing.assert_array_equal(oracle.emulate(inp, rows=0, split_tiles=True), oracle.emulate(inp, rows=0))
+    full = oracle.emulate(inp, rows=0).reshape(ref.shape)
+    full_st = oracle.emulate(inp, rows=0, split_tiles=True).reshape(ref.shape)
+    assert (full_st != full).mean() > 0.3
+    lut = oracle.Inputs(1, 2, 300, 300)   # 3 key tiles: the LUT recipe
+    np.testing.assert_array_equal(oracle.emulate(lut, rows=0, split_tiles=True), oracle.emulate(lut, rows=0))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_split_tile_order_full_sequence_accuracy(causal):
+    """The full-sequence split-tile order (every row, two 64-key streams merged) against fp64 attention: as accurate as
+    the reference's order (<= 1.10 x its mean error, no more bad elements), with and without the causal mask."""
+    inp = oracle.Inputs(1, 4, 512, 700, causal=causal)
+    ref = oracle.check_fp64(inp, oracle.emulate(inp, rows=0), rows=512)
+    st = oracle.check_fp64(inp, oracle.emulate(inp, rows=0, split_tiles=True), rows=512)
+    assert st["bad"] <= ref["bad"] and st["mean_err"] <= 1.10 * ref["mean_err"], (st, ref)
 
 
 def test_split_tile_order_duplicated_halves():
