@@ -4,7 +4,8 @@
 
 One step = one call of fmha_fwd_hd128_mxfp8_auto (dispatch + validate + launch, plus the combine on the KV-split
 path) on inputs already resident in HBM. Prints ONE JSON line. TFLOP/s = 4 B H S SK 128 / t (algorithmic,
-non-causal count, tests/gpu/ref_host.cpp:403); the causal workload counts the visible pairs.
+non-causal count, tests/gpu/ref_host.cpp:403); the causal workload counts only the visible
+(query, key) pairs, key <= query + SK - S (bottom-right mask).
 
 roofline: the dominant kernel's algorithmic FLOP per launch / its average duration, timed with HIP events on the
 launch stream, against the dense MXFP8 MFMA peak. cpu_baseline: the oracle's fp32 attention on the dequantised
