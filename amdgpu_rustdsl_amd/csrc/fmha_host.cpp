@@ -101,6 +101,13 @@ int t128_kernel(uint32_t SK, bool scaled, uint32_t* block) {
     return st ? (scaled ? K_T128ST_SC : K_T128ST) : (scaled ? K_T128_SC : K_T128);
 }
 
+// The one-call entry also runs the vs128 path on the split-tile kernel when its 256-row grid holds at most 128
+// blocks (half of the 256 CUs or fewer): on t128's 128-row grid the same shape fills twice the CUs. Not with the LUT
+// recipe (fewer than 4 key tiles), as for t128. The direct vs128 launcher keeps the 256-row kernel its grid names.
+bool vs128_split_tiles(int64_t B, int64_t H, int64_t S, int64_t SK) {
+    return (S + 255) / 256 * H * B <= 128 && t128_split_tiles((uint32_t)SK);
+}
+
 fmha_internal::ModuleCache<9> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
 
 int get_functions(hipFunction_t** out, char* err, size_t errlen) { return g_fmha.get(out, err, errlen); }
@@ -262,6 +269,12 @@ int fmha_mxfp8_validate_combine(const fmha_mxfp8_combine_args* a, const fmha_mxf
     return FMHA_OK;
 }
 
+int fmha_mxfp8_uses_split_tiles(int path, int64_t B, int64_t H, int64_t S, int64_t SK) {
+    if (path == FMHA_PATH_T128) return t128_split_tiles((uint32_t)SK) ? 1 : 0;
+    if (path == FMHA_PATH_VS128) return vs128_split_tiles(B, H, S, SK) ? 1 : 0;
+    return 0;
+}
+
 int fmha_mxfp8_select_path(int64_t B, int64_t H, int64_t S, int64_t SK, int* splits) {
     // dispatch.rs:494-511
     const i64 blocks256 = (S + 255) / 256 * H * B;
@@ -383,10 +396,17 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
         int rc = path == FMHA_PATH_VS128 ? fmha_mxfp8_validate_vs128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen)
                                          : fmha_mxfp8_validate_t128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen);
         if (rc != FMHA_OK) return rc;
-        uint32_t block = 512u;
-        const int kern = path == FMHA_PATH_VS128 ? (scaled ? K_VS128_SC : K_VS128) : t128_kernel((uint32_t)SK, scaled, &block);
-        return launch_raw(kern, &a, sizeof(a), gx, gy, (uint32_t)B, block, stream,
-                          err, errlen);
+        uint32_t block = 512u, kgx = gx;
+        int kern;
+        if (path == FMHA_PATH_T128) {
+            kern = t128_kernel((uint32_t)SK, scaled, &block);
+        } else if (vs128_split_tiles(B, H, S, SK)) {
+            kern = scaled ? K_T128ST_SC : K_T128ST;   // same kernarg layout, 128-row grid
+            kgx = (uint32_t)((S + 127) / 128);
+        } else {
+            kern = scaled ? K_VS128_SC : K_VS128;
+        }
+        return launch_raw(kern, &a, sizeof(a), kgx, gy, (uint32_t)B, block, stream, err, errlen);
     }
     // KV split: partials (fp32-sized rows, as ref_host.cpp:149 / ops.py:133) then the LSE, both in the workspace
     const i64 rows_total = B * S * H;

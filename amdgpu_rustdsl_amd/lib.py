@@ -91,6 +91,7 @@ _L.fmha_mxfp8_validate_t128.argtypes = [_P(Args), _P(BufferSizes), _u32, _u32, _
 _L.fmha_mxfp8_validate_kvsplit.argtypes = [_P(KvsplitArgs), _P(BufferSizes), _u32, _u32, _u32, _i64, _i64, _i64, _cp, _sz]
 _L.fmha_mxfp8_validate_combine.argtypes = [_P(CombineArgs), _P(BufferSizes), _u32, _u32, _u32, _cp, _sz]
 _L.fmha_mxfp8_select_path.argtypes = [_i64, _i64, _i64, _i64, _P(_c)]
+_L.fmha_mxfp8_uses_split_tiles.argtypes = [_c, _i64, _i64, _i64, _i64]
 _L.fmha_mxfp8_fill_args.argtypes = [_P(Args), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c, _c, _c, _c, _c]
 _L.fmha_mxfp8_fill_args.restype = None
 _L.fmha_mxfp8_workspace_bytes.argtypes = [_i64, _i64, _i64, _c]
@@ -111,7 +112,7 @@ _L.fmha_mxfp8_seq32_scale_bytes.argtypes = [_i64, _i64, _i64]
 _L.fmha_mxfp8_seq32_scale_bytes.restype = _sz
 
 EXPORTED = ["fmha_mxfp8_validate_vs128", "fmha_mxfp8_validate_t128", "fmha_mxfp8_validate_kvsplit", "fmha_mxfp8_validate_combine",
-            "fmha_mxfp8_select_path", "fmha_mxfp8_fill_args", "fmha_mxfp8_workspace_bytes", "fmha_mxfp8_launch_vs128",
+            "fmha_mxfp8_select_path", "fmha_mxfp8_uses_split_tiles", "fmha_mxfp8_fill_args", "fmha_mxfp8_workspace_bytes", "fmha_mxfp8_launch_vs128",
             "fmha_mxfp8_launch_t128", "fmha_mxfp8_launch_kvsplit", "fmha_mxfp8_launch_combine", "fmha_fwd_hd128_mxfp8_auto",
             "fmha_mxfp8_init", "fmha_mxfp8_version",
             "fmha_mxfp8_quantize_rows", "fmha_mxfp8_quantize_tensor", "fmha_mxfp8_quantize_seq32", "fmha_mxfp8_seq32_scale_bytes"]
@@ -138,6 +139,13 @@ def select_path(B, H, S, SK):
     sp = ctypes.c_int(0)
     path = _L.fmha_mxfp8_select_path(B, H, S, SK, ctypes.byref(sp))
     return PATH_NAMES[path], sp.value
+
+
+def uses_split_tiles(path, B, H, S, SK):
+    """Whether the one-call entry runs the full-sequence `path` ("vs128" / "t128") on the split-tile kernel."""
+    if path not in ("vs128", "t128"):
+        return False
+    return bool(_L.fmha_mxfp8_uses_split_tiles(PATH_IDS[path], B, H, S, SK))
 
 
 def workspace_bytes(B, H, S, splits):

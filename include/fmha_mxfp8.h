@@ -201,6 +201,13 @@ int fmha_mxfp8_validate_combine(const fmha_mxfp8_combine_args* a, const fmha_mxf
  * tests/gpu/ref_host.cpp:123-165). Returns FMHA_PATH_*; *splits = 0 unless KV split. */
 int fmha_mxfp8_select_path(int64_t B, int64_t H, int64_t S, int64_t SK, int* splits);
 
+/* Extension (no counterpart in the reference): 1 if fmha_fwd_hd128_mxfp8_auto runs the full-sequence `path`
+ * (FMHA_PATH_VS128 or FMHA_PATH_T128) on the split-tile kernel fmha_fwd_hd128_mxfp8_v3_t128_split_tiles (128-row
+ * blocks of 512 threads, the two wave groups splitting each tile's keys and merging at the end), else 0. t128: at
+ * least 4 key tiles. vs128: also a 256-row grid of at most 128 blocks. The split-tile order rounds differently from
+ * the reference's single stream per row; the path and its recipe are the reference's. */
+int fmha_mxfp8_uses_split_tiles(int path, int64_t B, int64_t H, int64_t S, int64_t SK);
+
 /* Fill the kernarg fields derived from a packed [B,S,H,128] / [B,SK,HK,128]
  * layout (the values ref_host.cpp:342-360 and ops.py:114-118 write). */
 void fmha_mxfp8_fill_args(fmha_mxfp8_args* a, void* o, const void* q, const void* k, const void* v,

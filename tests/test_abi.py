@@ -220,6 +220,30 @@ def test_select_path_matches_oracle():
     assert lib.select_path(1, 8, 128, 16384) == ("kvsplit", 4)
 
 
+def test_uses_split_tiles_rule():
+    """Which full-sequence launches of the one-call entry run on the split-tile kernel: t128 from 4 key tiles on;
+    vs128 when its 256-row grid holds at most 128 blocks, also from 4 key tiles on (the LUT recipe keeps the
+    single-stream kernels); never the KV split's own kernel."""
+    assert lib.uses_split_tiles("t128", 1, 8, 512, 512)
+    assert not lib.uses_split_tiles("t128", 1, 1, 256, 256)        # 2 key tiles: LUT recipe
+    assert not lib.uses_split_tiles("t128", 1, 8, 100, 384)        # 3 key tiles
+    assert lib.uses_split_tiles("t128", 1, 8, 100, 385)            # 4 key tiles
+    assert not lib.uses_split_tiles("vs128", 4, 8, 2048, 2048)     # 256 blocks: the whole chip already
+    assert lib.uses_split_tiles("vs128", 2, 8, 2048, 2048)         # 128 blocks
+    assert lib.uses_split_tiles("vs128", 4, 8, 1024, 1024)
+    assert lib.uses_split_tiles("vs128", 8, 8, 512, 512)
+    assert not lib.uses_split_tiles("vs128", 8, 8, 512, 384)       # LUT recipe
+    assert not lib.uses_split_tiles("vs128", 2, 8, 2100, 1000)     # 9 x 8 x 2 = 144 blocks
+    assert not lib.uses_split_tiles("vs128", 1, 8, 8192, 8192)
+    assert not lib.uses_split_tiles("kvsplit", 1, 8, 2048, 2048)
+    for B, H, S, SK in ((1, 8, 2048, 2048), (2, 8, 2048, 2048), (4, 8, 512, 512), (3, 5, 777, 1500), (1, 1, 1, 1)):
+        path = lib.select_path(B, H, S, SK)[0]
+        blocks256 = (S + 255) // 256 * H * B
+        ntiles = (SK + 127) // 128
+        want = path in ("t128", "vs128") and ntiles >= 4 and (path == "t128" or blocks256 <= 128)
+        assert lib.uses_split_tiles(path, B, H, S, SK) == want, (B, H, S, SK)
+
+
 def test_workspace_bytes():
     for B, H, S, sp in ((1, 8, 128, 8), (4, 8, 2048, 2), (3, 5, 77, 4)):
         assert lib.workspace_bytes(B, H, S, sp) == sp * B * S * H * (512 + 4)

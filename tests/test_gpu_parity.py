@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import oracle
+from amdgpu_rustdsl_amd import lib
 from tests import gpu_util
 
 pytestmark = pytest.mark.gpu
@@ -39,11 +40,12 @@ CASES = [
 
 def _emulated_bar(inp, splits, rows=ROWS, path=None, **kw):
     """The reference's error statistics (its order), and the emulation to compare element-wise with: the library's
-    own order, which differs from the reference's for KV-split blocks of at most 128 query rows and on the t128 path
-    (split tiles; not with the LUT recipe, which the emulation handles)."""
+    own order, which differs from the reference's for KV-split blocks of at most 128 query rows and where the one-call
+    entry runs a full-sequence path on the split-tile kernel (lib.uses_split_tiles; not with the LUT recipe, which
+    the emulation handles)."""
     emu = oracle.emulate(inp, splits=splits, rows=rows, **kw)
     ref_stats = oracle.check_fp64(inp, emu, rows=rows)
-    if splits or path == "t128":
+    if splits or (path is not None and lib.uses_split_tiles(path, inp.B, inp.H, inp.S, inp.SK)):
         emu = oracle.emulate(inp, splits=splits, rows=rows, split_tiles=True, **kw)
     return emu, ref_stats
 
@@ -166,7 +168,8 @@ def test_parity_v_seq32(gpu, case):
 
 
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("shape", [(1, 4, 4, 512, 640), (4, 8, 8, 1024, 1024)], ids=["t128", "vs128"])
+@pytest.mark.parametrize("shape", [(1, 4, 4, 512, 640), (4, 8, 8, 1024, 1024), (4, 8, 8, 2048, 2048)],
+                         ids=["t128", "vs128_split_tiles", "vs128"])
 def test_lse_output(gpu, shape, causal):
     """The optional natural-log LSE (kernarg 0x040): log sum_t exp(ln2 q.k_t) over the visible keys, against float64."""
     B, H, HK, S, SK = shape
@@ -297,3 +300,53 @@ def test_parity_t128_split_tiles(gpu, case):
         torch.cuda.synchronize()
         direct = o2.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
         np.testing.assert_array_equal(direct, out)
+
+
+# vs128 shapes whose 256-row grid holds at most 128 blocks: the one-call entry runs them on the split-tile kernel
+# (t128's 128-row grid, 512 threads); (name, B, H, HK, S, SK, causal, path forced or None)
+VS128_ST_CASES = [
+    ("B2H8S2048", 2, 8, 8, 2048, 2048, False, None),
+    ("B8H8S512", 8, 8, 8, 512, 512, False, None),
+    ("B4H8HK2_S1024_gqa4", 4, 8, 2, 1024, 1024, False, None),
+    ("B2H8S2048_SK1337", 2, 8, 8, 2048, 1337, False, None),
+    ("B1H4S700_SK900_forced", 1, 4, 4, 700, 900, False, "vs128"),
+    ("B2H4S1000_SK1000_causal_forced", 2, 4, 4, 1000, 1000, True, "vs128"),
+]
+
+
+@pytest.mark.parametrize("case", VS128_ST_CASES, ids=[c[0] for c in VS128_ST_CASES])
+def test_parity_vs128_split_tiles(gpu, case):
+    name, B, H, HK, S, SK, causal, force = case
+    print(f"[case] vs128 split tiles {name}", flush=True)
+    assert lib.uses_split_tiles("vs128", B, H, S, SK)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
+    out, used, _ = gpu_util.run(inp, gpu, path=force or "auto")
+    assert used[0] == "vs128"
+    rows = min(S, 256)
+    emu, ref_stats = _emulated_bar(inp, 0, rows=rows, path="vs128")
+    stats = oracle.check_fp64(inp, out, rows=rows)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
+    print(f"[case] vs128 split tiles {name} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
+    assert not np.isnan(oracle.bf16_to_f32(out)).any()
+    assert stats["bad"] <= ref_stats["bad"]
+    assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
+    assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
+    # no element-wise maximum under the causal mask, as in test_parity_causal: in the first rows a few keys carry the
+    # whole weight, so one fp8 rounding of P that the MFMA's inexact sum moves shifts an output by a few % of |V|
+    if not causal:
+        assert cmp["max_abs"] <= 0.05, cmp
+        # the direct vs128 launcher keeps the 256-row kernel its grid names (the single-stream order), correct here too
+        import ctypes, math, torch
+        q, k, v, qs, ks, vs = gpu_util.upload(inp, gpu)
+        o2 = torch.full((B, S, H, 128), float("nan"), dtype=torch.bfloat16, device=gpu)
+        a = lib.fill_args(o2.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), qs.data_ptr(), ks.data_ptr(), vs.data_ptr(),
+                          B, H, HK, S, SK)
+        st = torch.cuda.current_stream(gpu).cuda_stream
+        assert lib.raw.fmha_mxfp8_launch_vs128(ctypes.byref(a), math.ceil(S / 256), H, B, st) == 0
+        torch.cuda.synchronize()
+        direct = o2.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+        single = oracle.emulate(inp, rows=rows)
+        dcmp = gpu_util.compare_to_emulation(direct, single, inp, rows)
+        print(f"[case] vs128 direct launcher {name} vs-single-stream-emulation={dcmp}", flush=True)
+        assert dcmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), dcmp
+        assert dcmp["max_abs"] <= 0.05, dcmp
