@@ -94,7 +94,7 @@ enum { K_VS128 = 0, K_T128 = 1, K_KVSPLIT = 2, K_COMBINE = 3, K_VS128_SC = 4, K_
 
 // t128's shapes run on the split-tile kernel (512 threads) unless the whole sequence has fewer than 4 key tiles (the
 // LUT recipe, state.rs:75-77), which keeps the reference's order on the one-wave-per-SIMD kernel (256 threads)
-bool t128_split_tiles(uint32_t SK) { return (SK + 127u) / 128u >= 4u; }
+bool t128_split_tiles(int64_t SK) { return (SK + 127) / 128 >= 4; }
 int t128_kernel(uint32_t SK, bool scaled, uint32_t* block) {
     const bool st = t128_split_tiles(SK);
     *block = st ? 512u : 256u;
@@ -105,7 +105,7 @@ int t128_kernel(uint32_t SK, bool scaled, uint32_t* block) {
 // blocks (half of the 256 CUs or fewer): on t128's 128-row grid the same shape fills twice the CUs. Not with the LUT
 // recipe (fewer than 4 key tiles), as for t128. The direct vs128 launcher keeps the 256-row kernel its grid names.
 bool vs128_split_tiles(int64_t B, int64_t H, int64_t S, int64_t SK) {
-    return (S + 255) / 256 * H * B <= 128 && t128_split_tiles((uint32_t)SK);
+    return (S + 255) / 256 * H * B <= 128 && t128_split_tiles(SK);
 }
 
 fmha_internal::ModuleCache<9> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
@@ -270,7 +270,7 @@ int fmha_mxfp8_validate_combine(const fmha_mxfp8_combine_args* a, const fmha_mxf
 }
 
 int fmha_mxfp8_uses_split_tiles(int path, int64_t B, int64_t H, int64_t S, int64_t SK) {
-    if (path == FMHA_PATH_T128) return t128_split_tiles((uint32_t)SK) ? 1 : 0;
+    if (path == FMHA_PATH_T128) return t128_split_tiles(SK) ? 1 : 0;
     if (path == FMHA_PATH_VS128) return vs128_split_tiles(B, H, S, SK) ? 1 : 0;
     return 0;
 }
