@@ -143,7 +143,7 @@ def main():
     tflops = fl / (ms * 1e-3) / 1e12
 
     # dominant kernel alone: launched through the C ABI with a pre-validated kernarg, HIP events on its stream
-    kern_ms = kernel_ms(lib, q, k, v, qs, ks, vs, out, used, B, H, HK, S, SK, causal, stream, args.steps)
+    kern_ms, kern_name = kernel_ms(lib, q, k, v, qs, ks, vs, out, used, B, H, HK, S, SK, causal, stream, args.steps)
     kern_tflops = fl / (kern_ms * 1e-3) / 1e12
     traffic = None
     tfile = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
@@ -168,7 +168,7 @@ def main():
                    "causal": causal, "path": used[0], "splits": used[1], "pct_mxfp8_peak": round(100 * tflops / PEAK_MXFP8_TFLOPS, 2)},
         "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": PEAK_MXFP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(kern_tflops / PEAK_MXFP8_TFLOPS, 4), "traffic": traffic,
-                     "kernel": ("fmha_fwd_hd128_mxfp8_v3_" + used[0]), "kernel_ms": round(kern_ms, 5)},
+                     "kernel": kern_name, "kernel_ms": round(kern_ms, 5)},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(B, H, HK, S, SK, causal)
@@ -242,7 +242,8 @@ def main_quant(args, torch, lib, ops):
 
 
 def kernel_ms(lib, q, k, v, qs, ks, vs, out, used, B, H, HK, S, SK, causal, stream, steps):
-    """Average duration of the main kernel alone (no combine), launched through the C ABI launch entry."""
+    """Average duration of the main kernel alone (no combine), launched through the C ABI launch entry, and its
+    name."""
     import ctypes
     import torch
     from amdgpu_rustdsl_amd.ops import _cap
@@ -252,13 +253,19 @@ def kernel_ms(lib, q, k, v, qs, ks, vs, out, used, B, H, HK, S, SK, causal, stre
     sz = lib.BufferSizes(_cap(q), _cap(k), _cap(v), _cap(out), _cap(qs), _cap(ks), _cap(vs), 0, 0)
     st = stream.cuda_stream
     path, nsplit = used
+    kernel = "fmha_fwd_hd128_mxfp8_v3_" + path
     if path in ("vs128", "t128"):
-        rows = 256 if path == "vs128" else 128
-        grid = (math.ceil(S / rows), H, B)
-        rc, msg = lib.validate(path, a, sz, grid, HK=HK)
+        split_tiles = lib.uses_split_tiles(path, B, H, S, SK)
+        # the kernel the one-call entry runs: on split tiles (t128's grid, launched through the t128 entry, which
+        # picks the split-tile kernel from 4 key tiles on) or the path's own
+        on_t128 = path == "t128" or split_tiles
+        grid = (math.ceil(S / (128 if on_t128 else 256)), H, B)
+        rc, msg = lib.validate("t128" if on_t128 else "vs128", a, sz, grid, HK=HK)
         assert rc == 0, msg
-        launch = (lambda: lib.raw.fmha_mxfp8_launch_vs128(ctypes.byref(a), *grid, st)) if path == "vs128" else \
-                 (lambda: lib.raw.fmha_mxfp8_launch_t128(ctypes.byref(a), *grid, st))
+        launch = (lambda: lib.raw.fmha_mxfp8_launch_t128(ctypes.byref(a), *grid, st)) if on_t128 else \
+                 (lambda: lib.raw.fmha_mxfp8_launch_vs128(ctypes.byref(a), *grid, st))
+        if split_tiles:
+            kernel = "fmha_fwd_hd128_mxfp8_v3_t128_split_tiles"
     else:
         rows_total = B * S * H
         ws = torch.empty(lib.workspace_bytes(B, H, S, nsplit), dtype=torch.uint8, device=q.device)
@@ -281,7 +288,7 @@ def kernel_ms(lib, q, k, v, qs, ks, vs, out, used, B, H, HK, S, SK, causal, stre
         launch()
     e1.record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    return e0.elapsed_time(e1) / steps, kernel
 
 
 if __name__ == "__main__":
