@@ -16,6 +16,7 @@
 #include "module_cache.h"
 
 static_assert(sizeof(fmha_mxfp8_args) == 656, "kernarg size (vs128_abi.h:126)");
+static_assert(sizeof(fmha_mxfp8_params) == 168, "params layout (lib.py mirrors it)");
 static_assert(offsetof(fmha_mxfp8_args, ptr_o) == 0x000, "ptr_o");
 static_assert(offsetof(fmha_mxfp8_args, ptr_q) == 0x010, "ptr_q");
 static_assert(offsetof(fmha_mxfp8_args, ptr_k) == 0x020, "ptr_k");
@@ -393,9 +394,11 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
         a.ptr_lse = p->lse;
         const int rows = path == FMHA_PATH_VS128 ? 256 : 128;
         const uint32_t gx = (uint32_t)((S + rows - 1) / rows);
-        int rc = path == FMHA_PATH_VS128 ? fmha_mxfp8_validate_vs128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen)
-                                         : fmha_mxfp8_validate_t128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen);
-        if (rc != FMHA_OK) return rc;
+        if (!p->no_check) {
+            const int rc = path == FMHA_PATH_VS128 ? fmha_mxfp8_validate_vs128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen)
+                                                   : fmha_mxfp8_validate_t128(&a, &sz, gx, gy, (uint32_t)B, HK, err, errlen);
+            if (rc != FMHA_OK) return rc;
+        }
         uint32_t block = 512u, kgx = gx;
         int kern;
         if (path == FMHA_PATH_T128) {
@@ -427,7 +430,7 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     sz.ptr_ohat = (uint64_t)splits * rows_total * 512;
     sz.ptr_lse = (uint64_t)splits * rows_total * 4;
     const uint32_t gx = (uint32_t)((S + 255) / 256), gz = (uint32_t)(B * splits);
-    int rc = fmha_mxfp8_validate_kvsplit(&ka, &sz, gx, gy, gz, B, HK, 0, err, errlen);
+    int rc = p->no_check ? FMHA_OK : fmha_mxfp8_validate_kvsplit(&ka, &sz, gx, gy, gz, B, HK, 0, err, errlen);
     if (rc != FMHA_OK) return rc;
     rc = launch_raw(scaled ? K_KVSPLIT_SC : K_KVSPLIT, &ka, sizeof(ka), gx, gy, gz, 512, stream, err, errlen);
     if (rc != FMHA_OK) return rc;
@@ -440,8 +443,10 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     ca.splits = (uint32_t)splits | part_fmt;
     fmha_mxfp8_buffer_sizes csz = sz;
     csz.ptr_o = p->bytes_o;
-    rc = fmha_mxfp8_validate_combine(&ca, &csz, 0, 1, 1, err, errlen);
-    if (rc != FMHA_OK) return rc;
+    if (!p->no_check) {
+        rc = fmha_mxfp8_validate_combine(&ca, &csz, 0, 1, 1, err, errlen);
+        if (rc != FMHA_OK) return rc;
+    }
     const uint64_t cgrid = ((uint64_t)rows_total * 128 / 8 + 255) / 256;
     return launch_raw(K_COMBINE, &ca, sizeof(ca), (uint32_t)(cgrid ? cgrid : 1), 1, 1, 256, stream, err, errlen);
 }

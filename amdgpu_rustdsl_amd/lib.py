@@ -79,10 +79,11 @@ class Params(ctypes.Structure):
                 ("bytes_q_descale", _u64), ("bytes_k_descale", _u64), ("bytes_v_descale", _u64),
                 ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("HK", ctypes.c_int32), ("S", ctypes.c_int32), ("SK", ctypes.c_int32),
                 ("path", ctypes.c_int32), ("splits", ctypes.c_int32), ("causal", ctypes.c_int32),
-                ("f32_partials", ctypes.c_int32), ("v_seq32", ctypes.c_int32), ("softmax_scale", ctypes.c_float)]
+                ("f32_partials", ctypes.c_int32), ("v_seq32", ctypes.c_int32), ("softmax_scale", ctypes.c_float),
+                ("no_check", ctypes.c_int32)]
 
 
-assert ctypes.sizeof(Args) == 656 and ctypes.sizeof(KvsplitArgs) == 648 and ctypes.sizeof(CombineArgs) == 36
+assert ctypes.sizeof(Params) == 168 and ctypes.sizeof(Args) == 656 and ctypes.sizeof(KvsplitArgs) == 648 and ctypes.sizeof(CombineArgs) == 36
 
 _c, _i64, _sz, _cp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_char_p
 _P = ctypes.POINTER

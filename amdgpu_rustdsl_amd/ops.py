@@ -52,22 +52,28 @@ def _ws(device, stream, nbytes):
     return buf
 
 
-def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", splits=None, stream=None, lse=None, causal=False,
-                   partials="fp16", softmax_scale=None):
-    """MXFP8 attention forward, head dim 128 (``out = softmax(q k^T) v`` in base 2 with the E8M0 1x32 scales).
+def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", splits=None, specialize=True, stream=None, check=True,
+                   lse=None, causal=False, partials="fp16", softmax_scale=None):
+    """Attention forward on MXFP8 inputs with head dim 128, written into ``out``; returns the (path, splits) that ran.
 
-    q        [B, S, H, 128]   fp8 e4m3 (uint8 or float8_e4m3fn)   k, v [B, SK, HK, 128] (H = gqa HK, gqa a power of two <= 16)
-    q_scale  [B, S, H, 4]     E8M0 bytes          k_scale [B, SK, HK, 4]; both need the zeroed slack tail of the
-                                                   kernel contract (512 H 4 / 640 H 4 bytes behind the tensor)
-    v_scale  f32 V descale in a buffer of at least 4096 bytes, or (extension) a uint8 E8M0 tensor
-             [B, ceil(SK/32), HK, 128]: one scale per 32 keys per column (``quantize_v_seq32``'s output)
-    out      [B, S, H, 128]   bf16
-    path: "auto" | "vs128" | "t128" | "kvsplit" (``splits`` in {2, 4, 8}). Returns (path, splits).
-    Extensions (not in the reference): ``lse`` [B, H, S] f32 receives the natural-log LSE (vs128 / t128);
-    ``causal`` applies the bottom-right causal mask (key t visible to query i iff t <= i + SK - S);
-    ``partials="fp32"`` keeps the KV split's partial rows in f32 instead of the reference's fp16;
-    ``softmax_scale`` applies the scale in the kernel (``out = softmax(scale q k^T) v`` in natural log): q must then
-    be quantised without it. Default None: the reference's convention (the caller folds scale log2(e) into q).
+    Scores are base-2: the kernels compute softmax2(q . k) over dequantised q and k, so a caller that wants the usual
+    softmax(q k^T / sqrt(128)) multiplies q by log2(e) / sqrt(128) before quantising it (``fmha_fwd_bf16_via_mxfp8``
+    does this). Tensors, all on one device, contiguous:
+      q [B, S, H, 128] and k, v [B, SK, HK, 128]: e4m3 bytes (uint8 or float8_e4m3fn); H / HK is 1, 2, 4, 8 or 16.
+      q_scale [B, S, H, 4], k_scale [B, SK, HK, 4]: one E8M0 byte per 32 elements of each row. The kernels read up to
+        2048 H (q) and 2560 H (k) bytes past the end of these tensors, which must be zero: take them from
+        ``alloc_scales``.
+      v_scale: a float32 buffer of at least 4 KiB whose element 0 is V's descale; or, as an extension, uint8
+        [B, ceil(SK/32), HK, 128] holding one E8M0 per 32 keys and column (from ``quantize_v_seq32``).
+      out [B, S, H, 128] bf16.
+    path: "auto" picks the kernel the way the reference's dispatch does; "vs128", "t128" or "kvsplit" force one
+    (``splits``: 2, 4 or 8 for "kvsplit", default 4). ``stream``: a hipStream_t handle (default: torch's current
+    stream). ``specialize`` is accepted for callers of the reference op; the kernels take every shape at run time,
+    so there is nothing to specialise. ``check=False`` skips the host-side validate rules (buffer extents, strides,
+    grid) before the launch; the op's own shape checks still run.
+    Extensions: ``lse`` (float32 [B, H, S]) receives the natural-log log-sum-exp of each query row (vs128 / t128);
+    ``causal`` masks key t from query i unless t <= i + SK - S; ``partials="fp32"`` keeps the KV split's partial rows
+    in float32; ``softmax_scale`` makes the kernel apply scale * log2(e) to q . k itself (q then quantised unscaled).
     """
     if partials not in ("fp16", "fp32"):
         raise ValueError(f"fmha_fwd_mxfp8: partials must be 'fp16' or 'fp32', got {partials!r}")
@@ -110,6 +116,7 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     p.path, p.splits, p.causal = path_id, nsplit, int(bool(causal))
     p.f32_partials = int(partials == "fp32")
     p.v_seq32 = int(v_seq32)
+    p.no_check = int(not check)
     if softmax_scale is not None:
         if not float(softmax_scale) > 0.0:
             raise ValueError(f"fmha_fwd_mxfp8: softmax_scale must be positive, got {softmax_scale!r}")

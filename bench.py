@@ -7,8 +7,15 @@ path) on inputs already resident in HBM. Prints ONE JSON line. TFLOP/s = 4 B H S
 non-causal count, tests/gpu/ref_host.cpp:403); the causal workload counts only the visible
 (query, key) pairs, key <= query + SK - S (bottom-right mask).
 
-roofline: the dominant kernel's algorithmic FLOP per launch / its average duration, timed with HIP events on the
-launch stream, against the dense MXFP8 MFMA peak. cpu_baseline: the oracle's fp32 attention on the dequantised
+Timing. Before anything is timed the GPU runs the step for at least CLOCK_WARMUP_MS of wall time (the clock ramps for
+tens of milliseconds under this load, whatever --warmup says), then the --warmup untimed steps, then exactly --steps
+steps bracketed by synchronisations and HIP events on the launch stream: ms_per_step is their event time / steps
+(the wall time is reported beside it). The reference's own method (docs/perf-matrix.md:11: 100 launches, median of 5
+repetitions) is reported as `ref_method`.
+
+roofline: the dominant kernel's algorithmic FLOP per launch / its duration, against the dense MXFP8 MFMA peak. The
+kernel is launched alone through the C-ABI launcher, timed with HIP events on its stream, median of 5 repetitions of
+100 launches, interleaved with repetitions of the whole step so that both see the same clock. cpu_baseline: the oracle's fp32 attention on the dequantised
 inputs, all host cores, on a bounded sample of the same workload (rank 0, N = 1).
 """
 import argparse
@@ -24,6 +31,8 @@ sys.path.insert(0, ROOT)
 PEAK_MXFP8_TFLOPS = 5000.0      # MI355X dense MXFP8 MFMA peak, published figure (5.0 PFLOP/s)
 PEAK_HBM_GBS = 8000.0           # MI355X HBM3E
 REF_PUBLISHED_TFLOPS = 1811.8   # reference, B4H8S2048 vs128 (docs/perf-matrix.md:41)
+CLOCK_WARMUP_MS = 400.0         # wall time of untimed steps before any timing (the clock's ramp)
+REF_LAUNCHES, REF_REPS = 100, 5 # the reference's timing method (docs/perf-matrix.md:11)
 
 WORKLOADS = {
     # name: (B, H, HK, S, SK, causal, path, splits, description)
@@ -44,6 +53,20 @@ def flops_of(B, H, S, SK, causal):
     return 4.0 * B * H * vis * 128
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo) and the core count the OS reports."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    name = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{name} ({os.cpu_count()} logical CPUs on the host)"
+
+
 def cpu_baseline(B, H, HK, S, SK, causal, budget_s=12.0):
     """fp32 attention on the dequantised inputs (oracle), all host cores, bounded sample: whole (b, h) slices of the
     workload's shape with the first `rows` query rows, rows chosen so the run takes about `budget_s`."""
@@ -61,7 +84,7 @@ def cpu_baseline(B, H, HK, S, SK, causal, budget_s=12.0):
         fl = 4.0 * B * H * vis * 128
     else:
         fl = 4.0 * B * H * rows * SK * 128
-    return {"value": round(fl / secs / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+    return {"value": round(fl / secs / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"fp32 attention on dequantised MXFP8 inputs, B{B} H{H} SK{SK}, first {rows} of {S} query rows of every "
                       f"(b,h) ({fl / 1e9:.1f} GFLOP in {secs:.2f} s, {threads} threads, oracle/mxfp8_oracle.c)"}
 
@@ -69,9 +92,8 @@ def cpu_baseline(B, H, HK, S, SK, causal, budget_s=12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # the GPU clock ramps for several milliseconds under this load: 1000 warm-up steps (~40 ms) reach the steady clock
-    ap.add_argument("--steps", type=int, default=1000)
-    ap.add_argument("--warmup", type=int, default=1000)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
@@ -124,27 +146,60 @@ def main():
 
     assert step() == used
     torch.cuda.synchronize()
+    # the configs[1] line is quoted with the LSE saved: the natural-log LSE output (vs128 / t128) is on for the timed
+    # steps of the full-sequence paths
+    lse = None
+    if used[0] in ("vs128", "t128"):
+        lse = torch.empty(B, H, S, dtype=torch.float32, device=dev)
+        p.lse = lse.data_ptr()
+        assert step() == used
+
+    def timed(fn, n):
+        """Event time (ms) of n calls of fn on the stream, bracketed by synchronisations; the wall time beside it."""
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1), (time.perf_counter() - t0) * 1e3
+
+    # clock warm-up by wall time, then the --warmup steps, then exactly --steps timed steps
+    t_end = time.perf_counter() + CLOCK_WARMUP_MS / 1e3
+    clock_steps = 0
+    while time.perf_counter() < t_end:
+        for _ in range(50):
+            step()
+        clock_steps += 50
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_events = e0.elapsed_time(e1) / args.steps
-    ms_wall = wall * 1e3 / args.steps
-    ms = max(ms_events, ms_wall)
-    print(f"bench: {args.steps} steps, events {ms_events * 1e3:.2f} us/step, wall {ms_wall * 1e3:.2f} us/step", file=sys.stderr)
+    ev_ms, wall_ms = timed(step, args.steps)
+    ms = ev_ms / args.steps
+    ms_wall = wall_ms / args.steps
     fl = flops_of(B, H, S, SK, causal)
     tflops = fl / (ms * 1e-3) / 1e12
 
-    # dominant kernel alone: launched through the C ABI with a pre-validated kernarg, HIP events on its stream
-    kern_ms, kern_name = kernel_ms(lib, q, k, v, qs, ks, vs, out, used, B, H, HK, S, SK, causal, stream, args.steps)
+    # the dominant kernel alone through its C-ABI launcher, and the reference's timing method (median of 5 repetitions
+    # of 100 launches) for the step and the kernel, repetitions interleaved
+    launch, kern_name = kernel_launcher(lib, q, k, v, qs, ks, vs, out, lse, used, B, H, HK, S, SK, causal, stream)
+    rcs = []
+    kern = lambda: rcs.append(launch())
+    step_reps, kern_reps = [], []
+    for _ in range(REF_REPS):
+        step_reps.append(timed(step, REF_LAUNCHES)[0] / REF_LAUNCHES)
+        kern_reps.append(timed(kern, REF_LAUNCHES)[0] / REF_LAUNCHES)
+    assert all(rc == 0 for rc in rcs), f"kernel launches failed: {sorted(set(rcs))}"
+    med = lambda xs: sorted(xs)[len(xs) // 2]
+    ref_ms, kern_ms = med(step_reps), med(kern_reps)
     kern_tflops = fl / (kern_ms * 1e-3) / 1e12
+    print(f"bench: clock warm-up {clock_steps} steps; {args.steps} steps: events {ms * 1e3:.2f} us/step, wall {ms_wall * 1e3:.2f} "
+          f"us/step; reference method: step {ref_ms * 1e3:.2f} us, kernel {kern_name} {kern_ms * 1e3:.2f} us "
+          f"(reps step {[round(x * 1e3, 2) for x in step_reps]}, kernel {[round(x * 1e3, 2) for x in kern_reps]})", file=sys.stderr)
+    if kern_ms > ms:
+        print(f"bench: WARNING kernel_ms {kern_ms:.5f} > ms_per_step {ms:.5f}", file=sys.stderr)
     traffic = None
     tfile = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
     if os.path.exists(tfile):
@@ -158,14 +213,20 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_warmup": {"ms": CLOCK_WARMUP_MS, "steps": clock_steps},
         "ms_per_step": round(ms, 5),
+        "ms_per_step_wall": round(ms_wall, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(tflops / REF_PUBLISHED_TFLOPS, 4) if args.workload == "cfg2" else None,
+        "ref_method": {"launches": REF_LAUNCHES, "reps": REF_REPS, "ms_per_step": round(ref_ms, 5),
+                       "value": round(fl / (ref_ms * 1e-3) / 1e12, 2),
+                       "vs_baseline": round(fl / (ref_ms * 1e-3) / 1e12 / REF_PUBLISHED_TFLOPS, 4) if args.workload == "cfg2" else None},
         "dtype": "e4m3 (MXFP8, E8M0/32 scales, fp32 accumulate)",
         "data": "synthetic: N(0,1) Q/K/V quantised to MXFP8 like the reference's REF_DATA=normal generator, drawn on the GPU",
         "config": {"workload": f"fmha_fwd_hd128_mxfp8_auto {desc}", "B": B, "H": H, "HK": HK, "S": S, "SK": SK,
-                   "causal": causal, "path": used[0], "splits": used[1], "pct_mxfp8_peak": round(100 * tflops / PEAK_MXFP8_TFLOPS, 2)},
+                   "causal": causal, "path": used[0], "splits": used[1], "lse": lse is not None,
+                   "pct_mxfp8_peak": round(100 * tflops / PEAK_MXFP8_TFLOPS, 2)},
         "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": PEAK_MXFP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(kern_tflops / PEAK_MXFP8_TFLOPS, 4), "traffic": traffic,
                      "kernel": kern_name, "kernel_ms": round(kern_ms, 5)},
@@ -241,15 +302,15 @@ def main_quant(args, torch, lib, ops):
     print(json.dumps(line), flush=True)
 
 
-def kernel_ms(lib, q, k, v, qs, ks, vs, out, used, B, H, HK, S, SK, causal, stream, steps):
-    """Average duration of the main kernel alone (no combine), launched through the C ABI launch entry, and its
-    name."""
+def kernel_launcher(lib, q, k, v, qs, ks, vs, out, lse, used, B, H, HK, S, SK, causal, stream):
+    """A launch of the main kernel alone (no combine) through its C-ABI launcher, validated once, and its name."""
     import ctypes
     import torch
     from amdgpu_rustdsl_amd.ops import _cap
     a = lib.fill_args(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), qs.data_ptr(), ks.data_ptr(), vs.data_ptr(),
                       B, H, HK, S, SK)
     a.flags = 1 if causal else 0
+    a.ptr_lse = lse.data_ptr() if lse is not None else None
     sz = lib.BufferSizes(_cap(q), _cap(k), _cap(v), _cap(out), _cap(qs), _cap(ks), _cap(vs), 0, 0)
     st = stream.cuda_stream
     path, nsplit = used
@@ -278,17 +339,12 @@ def kernel_ms(lib, q, k, v, qs, ks, vs, out, used, B, H, HK, S, SK, causal, stre
         sz.ptr_ohat, sz.ptr_lse = nsplit * rows_total * 512, nsplit * rows_total * 4
         rc, msg = lib.validate("kvsplit", ka, sz, grid, B=B, HK=HK, KL=0)
         assert rc == 0, msg
-        launch = lambda: lib.raw.fmha_mxfp8_launch_kvsplit(ctypes.byref(ka), *grid, st)
+        # (the closure holds the workspace tensor, so it lives as long as the launcher)
+        launch = lambda ws=ws: lib.raw.fmha_mxfp8_launch_kvsplit(ctypes.byref(ka), *grid, st)
     for _ in range(20):
         assert launch() == 0
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
-        launch()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps, kernel
+    return launch, kernel
 
 
 if __name__ == "__main__":

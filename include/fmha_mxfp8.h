@@ -246,6 +246,9 @@ typedef struct fmha_mxfp8_params {
     int32_t v_seq32;           /* 0 = v_descale is one f32 (the reference's); 1 = E8M0 per 32 keys per column (extension) */
     float softmax_scale;       /* 0 = the reference's convention (the scale is folded into Q before quantisation);
                                   > 0 = applied in the kernel (FMHA_FLAG_SCALE / FMHA_KVS_SCALE, extension) */
+    int32_t no_check;          /* 0 = run the validate rules before launching (the default); 1 = skip them, as the
+                                  reference op's check=False does (python/amdgpu_jit/ops.py:88): the caller then
+                                  vouches for the buffer extents and strides */
 } fmha_mxfp8_params;
 
 /* fmha_fwd_hd128_mxfp8_auto: dispatch + validate + launch (+ combine), all on

@@ -337,3 +337,33 @@ def test_code_objects_have_no_calls():
         if not os.path.exists(path):
             pytest.skip(f"{name} not built")
         assert build.code_object_calls(path) == [], name
+
+
+def test_op_signature_accepts_reference_kwargs():
+    """A caller of the reference op (python/amdgpu_jit/ops.py:88) passes path, splits, specialize, stream and check by
+    keyword; the op takes them with the same defaults."""
+    import inspect
+    from amdgpu_rustdsl_amd import ops
+    sig = inspect.signature(ops.fmha_fwd_mxfp8)
+    want = {"path": "auto", "splits": None, "specialize": True, "stream": None, "check": True}
+    for name, default in want.items():
+        assert sig.parameters[name].default == default, name
+        assert sig.parameters[name].kind == inspect.Parameter.KEYWORD_ONLY, name
+    assert list(sig.parameters)[:7] == ["q", "k", "v", "q_scale", "k_scale", "v_scale", "out"]
+
+
+def test_no_check_skips_validate():
+    """params.no_check (the op's check=False) skips the validate rules: a too-small output buffer is an extent error
+    with the check and goes on to the launch without it (which, with no GPU here, reports the missing device)."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("the unchecked call would launch on the GPU")
+    err = ctypes.create_string_buffer(256)
+    po, so = ctypes.c_int(-1), ctypes.c_int(-1)
+    p = _params(path=0)
+    p.bytes_o = 16
+    rc = lib.raw.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(p), None, 0, None, ctypes.byref(po), ctypes.byref(so), err, 256)
+    assert rc == lib.FMHA_ERR_EXTENT and b"GV-HOST-EXTENT" in err.value, (rc, err.value)
+    p.no_check = 1
+    rc = lib.raw.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(p), None, 0, None, ctypes.byref(po), ctypes.byref(so), err, 256)
+    assert rc in (lib.FMHA_ERR_NO_DEVICE, lib.FMHA_ERR_HIP), (rc, err.value)
