@@ -59,9 +59,12 @@ def build(verbose=False):
         if calls:
             os.remove(co)
             raise RuntimeError(f"{co}: a kernel calls an outlined function ({calls[0]}); force-inline it")
+    # the allocation-free entry is single-source HIP (its device array is registered with the runtime at load time)
+    noalloc_o = os.path.join(OUT, "fmha_noalloc.o")
+    _run([hipcc, *HIP_FLAGS, "-fPIC", "-c", os.path.join(CSRC, "fmha_noalloc.hip"), "-o", noalloc_o])
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
           "-I" + os.path.join(ROCM, "include"), '-DFMHA_HSACO_PATH="%s"' % HSACO, '-DMXQ_HSACO_PATH="%s"' % QHSACO,
-          os.path.join(CSRC, "fmha_host.cpp"), os.path.join(CSRC, "quant_host.cpp"), "-L" + os.path.join(ROCM, "lib"), "-lamdhip64",
+          os.path.join(CSRC, "fmha_host.cpp"), os.path.join(CSRC, "quant_host.cpp"), noalloc_o, "-L" + os.path.join(ROCM, "lib"), "-lamdhip64",
           "-Wl,-rpath," + os.path.join(ROCM, "lib"), "-o", LIB])
     if verbose:
         print("built", HSACO, os.path.getsize(HSACO), "bytes;", LIB, os.path.getsize(LIB), "bytes")

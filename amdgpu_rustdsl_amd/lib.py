@@ -102,6 +102,7 @@ _L.fmha_mxfp8_launch_t128.argtypes = [_P(Args), _u32, _u32, _u32, _vp]
 _L.fmha_mxfp8_launch_kvsplit.argtypes = [_P(KvsplitArgs), _u32, _u32, _u32, _vp]
 _L.fmha_mxfp8_launch_combine.argtypes = [_P(CombineArgs), _u32, _vp]
 _L.fmha_fwd_hd128_mxfp8_auto.argtypes = [_P(Params), _vp, _sz, _vp, _P(_c), _P(_c), _cp, _sz]
+_L.fmha_fwd_hd128_mxfp8_auto_noalloc.argtypes = [_P(Params), _vp, _P(_c), _P(_c), _cp, _sz]
 _L.fmha_mxfp8_init.argtypes = [_cp, _sz]
 _L.fmha_mxfp8_version.restype = _cp
 _L.fmha_mxfp8_version.argtypes = []
@@ -115,6 +116,7 @@ _L.fmha_mxfp8_seq32_scale_bytes.restype = _sz
 EXPORTED = ["fmha_mxfp8_validate_vs128", "fmha_mxfp8_validate_t128", "fmha_mxfp8_validate_kvsplit", "fmha_mxfp8_validate_combine",
             "fmha_mxfp8_select_path", "fmha_mxfp8_uses_split_tiles", "fmha_mxfp8_fill_args", "fmha_mxfp8_workspace_bytes", "fmha_mxfp8_launch_vs128",
             "fmha_mxfp8_launch_t128", "fmha_mxfp8_launch_kvsplit", "fmha_mxfp8_launch_combine", "fmha_fwd_hd128_mxfp8_auto",
+            "fmha_fwd_hd128_mxfp8_auto_noalloc",
             "fmha_mxfp8_init", "fmha_mxfp8_version",
             "fmha_mxfp8_quantize_rows", "fmha_mxfp8_quantize_tensor", "fmha_mxfp8_quantize_seq32", "fmha_mxfp8_seq32_scale_bytes"]
 
@@ -188,6 +190,18 @@ def run_auto(params, workspace=None, workspace_bytes=0, stream=None):
     path, splits = ctypes.c_int(-1), ctypes.c_int(0)
     rc = _L.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(params), workspace, workspace_bytes, stream, ctypes.byref(path),
                                       ctypes.byref(splits), buf, 512)
+    check(rc, buf)
+    return PATH_NAMES[path.value], splits.value
+
+
+NOALLOC_SCRATCH_BYTES = 33816576   # FMHA_NOALLOC_SCRATCH_BYTES
+
+
+def run_auto_noalloc(params, stream=None):
+    """fmha_fwd_hd128_mxfp8_auto_noalloc (no workspace argument); returns (path name, splits)."""
+    buf = _errbuf()
+    path, splits = ctypes.c_int(-1), ctypes.c_int(0)
+    rc = _L.fmha_fwd_hd128_mxfp8_auto_noalloc(ctypes.byref(params), stream, ctypes.byref(path), ctypes.byref(splits), buf, 512)
     check(rc, buf)
     return PATH_NAMES[path.value], splits.value
 

@@ -259,6 +259,19 @@ typedef struct fmha_mxfp8_params {
 int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_t workspace_bytes,
                               void* stream, int* path_out, int* splits_out, char* err, size_t errlen);
 
+/* Allocation-free variant of fmha_fwd_hd128_mxfp8_auto. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory or pass a workspace (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). The KV split's workspace is a device array of FMHA_NOALLOC_SCRATCH_BYTES inside the library
+ * instead of a caller's buffer, one per device, held until the process ends; a shape whose split needs more is
+ * rejected with FMHA_ERR_WORKSPACE. The largest workspace the auto dispatch asks for is 2 splits x 32768 rows x 516 B
+ * (blocks256 <= 128 bounds B S H to 32768): exactly this size. The first call on a device looks the array up and loads
+ * the code objects (fmha_mxfp8_init); later calls call no allocating routine and no hipMalloc/hipFree. Calls on one
+ * device share its array: calls that overlap on one device (unordered streams) race. Otherwise identical to
+ * fmha_fwd_hd128_mxfp8_auto (same params, rules, errors and kernels). */
+#define FMHA_NOALLOC_SCRATCH_BYTES 33816576u
+int fmha_fwd_hd128_mxfp8_auto_noalloc(const fmha_mxfp8_params* p, void* stream, int* path_out, int* splits_out,
+                                      char* err, size_t errlen);
+
 /* Loads the embedded code object on the current device (done lazily by the
  * launch calls; exposed so a caller can fail early). */
 int fmha_mxfp8_init(char* err, size_t errlen);

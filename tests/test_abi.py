@@ -367,3 +367,15 @@ def test_no_check_skips_validate():
     p.no_check = 1
     rc = lib.raw.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(p), None, 0, None, ctypes.byref(po), ctypes.byref(so), err, 256)
     assert rc in (lib.FMHA_ERR_NO_DEVICE, lib.FMHA_ERR_HIP), (rc, err.value)
+
+
+def test_noalloc_rejects_oversized_split_before_gpu_work():
+    """fmha_fwd_hd128_mxfp8_auto_noalloc refuses a split whose workspace exceeds its scratch array (the largest the
+    auto dispatch asks for) before touching the device."""
+    assert lib.NOALLOC_SCRATCH_BYTES == 2 * 32768 * 516 == max(
+        lib.workspace_bytes(B, H, S, 2) for B, H, S in ((1, 8, 4096), (2, 16, 1024), (1, 1, 32768)))
+    p = _params(path=2, splits=8, S=2048, SK=2048)
+    err = ctypes.create_string_buffer(256)
+    po, so = ctypes.c_int(-1), ctypes.c_int(-1)
+    rc = lib.raw.fmha_fwd_hd128_mxfp8_auto_noalloc(ctypes.byref(p), None, ctypes.byref(po), ctypes.byref(so), err, 256)
+    assert rc == lib.FMHA_ERR_WORKSPACE and b"GV-HOST-WORKSPACE" in err.value, (rc, err.value)
