@@ -596,3 +596,22 @@ def test_qk_scale_mantissa(splits):
     u = np.ascontiguousarray(f32, dtype=np.float32).view(np.uint32)
     as_bf16 = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)   # round to nearest even
     assert oracle.check_fp64(inp, as_bf16, rows=S)["mean_err"] < 0.5 * got["mean_err"]
+
+
+def test_generator_matches_reference_harness():
+    """The oracle's input generator is byte-identical to the reference harness's own (tests/gpu/ref_host.cpp:183-263),
+    in all three data modes (lcg palette, uniform bytes, normal MXFP8) and on every shape of run_ref.sh:57, the
+    determinism list and the BASELINE configs: tests/golden/ref_inputs.json holds the SHA-256 of each buffer that the
+    reference's harness, built from its source, dumped (tests/golden/make_ref_inputs_fixture.py)."""
+    import hashlib
+    import json
+    with open(os.path.join(os.path.dirname(__file__), "golden", "ref_inputs.json")) as f:
+        fx = json.load(f)
+    assert len(fx["entries"]) >= 50
+    for e in fx["entries"]:
+        inp = oracle.Inputs(e["B"], e["H"], e["S"], e["SK"], HK=e["H"] // e["gqa"], mode=e["mode"])
+        for ext, arr in (("q", inp.q), ("k", inp.k), ("v", inp.v), ("qs", inp.qs), ("ks", inp.ks)):
+            want = e["digests"][ext]
+            data = np.ascontiguousarray(arr).tobytes()
+            assert len(data) == want["bytes"], (e, ext)
+            assert hashlib.sha256(data).hexdigest() == want["sha256"], (e["B"], e["H"], e["S"], e["SK"], e["mode"], ext)
