@@ -338,9 +338,11 @@ int fmha_mxfp8_launch_vs128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, 
     return launch_raw((a->flags & FMHA_FLAG_SCALE) ? K_VS128_SC : K_VS128, a, sizeof(*a), gx, gy, gz, 512, stream, nullptr, 0);
 }
 int fmha_mxfp8_launch_t128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream) {
-    uint32_t block;
-    const int kern = t128_kernel(a->s_kv_seq_len, (a->flags & FMHA_FLAG_SCALE) != 0, &block);
-    return launch_raw(kern, a, sizeof(*a), gx, gy, gz, block, stream, nullptr, 0);
+    // the reference-named kernel under its own contract: 256 threads (t128_abi.h)
+    return launch_raw((a->flags & FMHA_FLAG_SCALE) ? K_T128_SC : K_T128, a, sizeof(*a), gx, gy, gz, 256, stream, nullptr, 0);
+}
+int fmha_mxfp8_launch_t128_split_tiles(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream) {
+    return launch_raw((a->flags & FMHA_FLAG_SCALE) ? K_T128ST_SC : K_T128ST, a, sizeof(*a), gx, gy, gz, 512, stream, nullptr, 0);
 }
 int fmha_mxfp8_launch_kvsplit(const fmha_mxfp8_kvsplit_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream) {
     return launch_raw((a->kvs_splits & FMHA_KVS_SCALE) ? K_KVSPLIT_SC : K_KVSPLIT, a, sizeof(*a), gx, gy, gz, 512, stream, nullptr, 0);

@@ -99,6 +99,7 @@ _L.fmha_mxfp8_workspace_bytes.argtypes = [_i64, _i64, _i64, _c]
 _L.fmha_mxfp8_workspace_bytes.restype = _sz
 _L.fmha_mxfp8_launch_vs128.argtypes = [_P(Args), _u32, _u32, _u32, _vp]
 _L.fmha_mxfp8_launch_t128.argtypes = [_P(Args), _u32, _u32, _u32, _vp]
+_L.fmha_mxfp8_launch_t128_split_tiles.argtypes = [_P(Args), _u32, _u32, _u32, _vp]
 _L.fmha_mxfp8_launch_kvsplit.argtypes = [_P(KvsplitArgs), _u32, _u32, _u32, _vp]
 _L.fmha_mxfp8_launch_combine.argtypes = [_P(CombineArgs), _u32, _vp]
 _L.fmha_fwd_hd128_mxfp8_auto.argtypes = [_P(Params), _vp, _sz, _vp, _P(_c), _P(_c), _cp, _sz]
@@ -115,7 +116,7 @@ _L.fmha_mxfp8_seq32_scale_bytes.restype = _sz
 
 EXPORTED = ["fmha_mxfp8_validate_vs128", "fmha_mxfp8_validate_t128", "fmha_mxfp8_validate_kvsplit", "fmha_mxfp8_validate_combine",
             "fmha_mxfp8_select_path", "fmha_mxfp8_uses_split_tiles", "fmha_mxfp8_fill_args", "fmha_mxfp8_workspace_bytes", "fmha_mxfp8_launch_vs128",
-            "fmha_mxfp8_launch_t128", "fmha_mxfp8_launch_kvsplit", "fmha_mxfp8_launch_combine", "fmha_fwd_hd128_mxfp8_auto",
+            "fmha_mxfp8_launch_t128", "fmha_mxfp8_launch_t128_split_tiles", "fmha_mxfp8_launch_kvsplit", "fmha_mxfp8_launch_combine", "fmha_fwd_hd128_mxfp8_auto",
             "fmha_fwd_hd128_mxfp8_auto_noalloc",
             "fmha_mxfp8_init", "fmha_mxfp8_version",
             "fmha_mxfp8_quantize_rows", "fmha_mxfp8_quantize_tensor", "fmha_mxfp8_quantize_seq32", "fmha_mxfp8_seq32_scale_bytes"]

@@ -317,14 +317,17 @@ def kernel_launcher(lib, q, k, v, qs, ks, vs, out, lse, used, B, H, HK, S, SK, c
     kernel = "fmha_fwd_hd128_mxfp8_v3_" + path
     if path in ("vs128", "t128"):
         split_tiles = lib.uses_split_tiles(path, B, H, S, SK)
-        # the kernel the one-call entry runs: on split tiles (t128's grid, launched through the t128 entry, which
-        # picks the split-tile kernel from 4 key tiles on) or the path's own
+        # the kernel the one-call entry runs: the split-tile kernel (t128's grid, 512 threads) or the path's own
         on_t128 = path == "t128" or split_tiles
         grid = (math.ceil(S / (128 if on_t128 else 256)), H, B)
         rc, msg = lib.validate("t128" if on_t128 else "vs128", a, sz, grid, HK=HK)
         assert rc == 0, msg
-        launch = (lambda: lib.raw.fmha_mxfp8_launch_t128(ctypes.byref(a), *grid, st)) if on_t128 else \
-                 (lambda: lib.raw.fmha_mxfp8_launch_vs128(ctypes.byref(a), *grid, st))
+        if split_tiles:
+            launch = lambda: lib.raw.fmha_mxfp8_launch_t128_split_tiles(ctypes.byref(a), *grid, st)
+        elif on_t128:
+            launch = lambda: lib.raw.fmha_mxfp8_launch_t128(ctypes.byref(a), *grid, st)
+        else:
+            launch = lambda: lib.raw.fmha_mxfp8_launch_vs128(ctypes.byref(a), *grid, st)
         if split_tiles:
             kernel = "fmha_fwd_hd128_mxfp8_v3_t128_split_tiles"
     else:

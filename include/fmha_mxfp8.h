@@ -226,6 +226,11 @@ size_t fmha_mxfp8_workspace_bytes(int64_t B, int64_t H, int64_t S, int splits);
  * (a hipStream_t, NULL = the null stream). Returns FMHA_OK or FMHA_ERR_HIP. */
 int fmha_mxfp8_launch_vs128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream);
 int fmha_mxfp8_launch_t128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream);
+/* Extension (no counterpart in the reference): the split-tile kernel fmha_fwd_hd128_mxfp8_v3_t128_split_tiles on
+ * t128's grid (ceil(S/128), H, B) and kernarg layout, 512 threads; the two wave groups split each key tile and merge
+ * at the end (the order fmha_mxfp8_uses_split_tiles names). fmha_fwd_hd128_mxfp8_auto runs it for t128's shapes with
+ * at least 4 key tiles and for vs128's shapes whose 256-row grid has at most 128 blocks. */
+int fmha_mxfp8_launch_t128_split_tiles(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream);
 int fmha_mxfp8_launch_kvsplit(const fmha_mxfp8_kvsplit_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream);
 int fmha_mxfp8_launch_combine(const fmha_mxfp8_combine_args* a, uint32_t gx, void* stream);
 

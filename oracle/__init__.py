@@ -79,6 +79,10 @@ def lib():
         L.mxo_emulate_ex.restype = None
         L.mxo_emulate_ex.argtypes = [ctypes.POINTER(Problem), i, i, vp, vp, vp, i, i, i]
         L.mxo_combine_f32.restype = None
+        L.mxo_check_fp64_rows.restype = CheckResult
+        L.mxo_check_fp64_rows.argtypes = [ctypes.POINTER(Problem), vp, vp, i, i]
+        L.mxo_emulate_rows.restype = None
+        L.mxo_emulate_rows.argtypes = [ctypes.POINTER(Problem), i, vp, i, vp, i, i, i]
         L.mxo_combine_f32.argtypes = [vp, vp, vp, ctypes.c_long, i]
         L.mxo_quant_rows_bf16.argtypes = [vp, ctypes.c_long, f, vp, vp]
         L.mxo_quant_rows_bf16.restype = None
@@ -137,21 +141,46 @@ class Inputs:
         return self.B * self.S * self.H * D
 
 
+def row_list(S, rows):
+    """Normalises a row selection: an int n means the first n rows (as the reference's check samples them); a
+    sequence names the rows. Returns an int32 array of distinct rows in [0, S)."""
+    if isinstance(rows, (int, np.integer)):
+        return np.arange(min(int(rows), S) if rows > 0 else S, dtype=np.int32)
+    r = np.unique(np.asarray(rows, dtype=np.int32))
+    assert r.size and r.min() >= 0 and r.max() < S, "rows outside [0, S)"
+    return r
+
+
+def first_and_last(S, n=64):
+    """The first n and the last n query rows (the reference's 64-row sample plus the end of the sequence: the last
+    query tile, the ragged tail and, under the bottom-right causal mask, the rows that see every key tile)."""
+    return row_list(S, np.concatenate([np.arange(min(n, S)), np.arange(max(0, S - n), S)]))
+
+
 def check_fp64(inp, out_bf16, rows=64, threads=0):
-    """ref_host.cpp:436-471 statistics of a bf16 output (uint16 array)."""
+    """ref_host.cpp:436-471 statistics of a bf16 output (uint16 array) over `rows` (the first n, or a list)."""
     out = np.ascontiguousarray(out_bf16, dtype=np.uint16).reshape(-1)
     assert out.size == inp.out_elems
     p = inp.problem()
-    return lib().mxo_check_fp64(ctypes.byref(p), _ptr(out), int(rows), int(threads)).as_dict()
+    if isinstance(rows, (int, np.integer)):
+        return lib().mxo_check_fp64(ctypes.byref(p), _ptr(out), int(rows), int(threads)).as_dict()
+    lst = row_list(inp.S, rows)
+    return lib().mxo_check_fp64_rows(ctypes.byref(p), _ptr(out), _ptr(lst), int(lst.size), int(threads)).as_dict()
 
 
 def emulate(inp, splits=0, rows=64, threads=0, partials=False, f32_partials=False, split_tiles=False):
-    """Bit-level model of the reference kernels on the first ``rows`` rows of every (b, h).
+    """Bit-level model of the reference kernels on the first ``rows`` rows of every (b, h) (or the listed rows).
     Returns the bf16 output (uint16, rows not emulated are 0), and with ``partials`` also (ohat, lse f32): ohat fp16
     (uint16), or f32 with ``f32_partials`` (the FMHA_KVS_F32_PARTIALS extension). ``split_tiles`` models the library's
     order (two 64-key streams per tile, merged; not with the LUT recipe) instead of the reference's: for KV-split blocks
     of at most 128 query rows, and with ``splits=0`` for every row (the t128 path's split-tile kernel)."""
     out = np.zeros(inp.out_elems, np.uint16)
+    if not isinstance(rows, (int, np.integer)):
+        assert not partials, "partials are emulated for leading rows only"
+        lst = row_list(inp.S, rows)
+        lib().mxo_emulate_rows(ctypes.byref(inp.problem()), int(splits), _ptr(lst), int(lst.size), _ptr(out),
+                               int(bool(f32_partials)), int(bool(split_tiles)), int(threads))
+        return out
     ohat = lse = None
     if partials and splits:
         rows_total = inp.B * inp.S * inp.H

@@ -330,6 +330,7 @@ typedef struct {
     const mxo_problem* p;
     const uint16_t* o;
     int rows;
+    const int* list; /* the checked rows: list[0 .. rows) (NULL: rows 0 .. rows - 1) */
     double* worst;   /* per (b,h) */
     double* sum_abs;
     double* max_ref;
@@ -347,7 +348,8 @@ static void check_item(const void* vctx, long item) {
     double qd[D];
     double worst = 0, sum_abs = 0, max_ref = 0;
     uint64_t bad = 0, cnt = 0;
-    for (int i = 0; i < p->S && i < c->rows; ++i) {
+    for (int ii = 0; ii < c->rows && (c->list || ii < p->S); ++ii) {
+        const int i = c->list ? c->list[ii] : ii;
         for (int kk = 0; kk < D; ++kk)
             qd[kk] = mxo_e4m3_decode(p->q[(((size_t)b * p->S + i) * p->H + h) * D + kk]) *
                      ldexp(1.0, (int)p->qs[(((size_t)b * p->S + i) * p->H + h) * 4 + kk / 32] - 127);
@@ -382,8 +384,12 @@ static void check_item(const void* vctx, long item) {
 }
 
 mxo_check_result mxo_check_fp64(const mxo_problem* p, const uint16_t* out_bf16, int rows, int threads) {
+    return mxo_check_fp64_rows(p, out_bf16, NULL, rows, threads);
+}
+
+mxo_check_result mxo_check_fp64_rows(const mxo_problem* p, const uint16_t* out_bf16, const int* row_list, int rows, int threads) {
     const long n = (long)p->B * p->H;
-    check_ctx c = {p, out_bf16, rows, calloc(n, 8), calloc(n, 8), calloc(n, 8), calloc(n, 8), calloc(n, 8)};
+    check_ctx c = {p, out_bf16, rows, row_list, calloc(n, 8), calloc(n, 8), calloc(n, 8), calloc(n, 8), calloc(n, 8)};
     run_parallel(threads, n, &c, check_item);
     mxo_check_result r = {0, 0, 0, 0, 0};
     double sum_abs = 0;
@@ -631,6 +637,7 @@ typedef struct {
     float* lse;
     int f32_partials;
     int split_tiles;     /* 1: the library's split-tile order where it applies (KV split only) */
+    const int* list;     /* the emulated rows: list[0 .. rows) (NULL: rows 0 .. rows - 1) */
 } emu_ctx;
 
 static void emu_item(const void* vctx, long item) {
@@ -638,7 +645,7 @@ static void emu_item(const void* vctx, long item) {
     const mxo_problem* p = c->p;
     const int rows = c->rows;
     const long bh = item / rows;
-    const int i = (int)(item % rows);
+    const int i = c->list ? c->list[item % rows] : (int)(item % rows);
     const int b = (int)(bh / p->H), h = (int)(bh % p->H);
     const int kvh = h / (p->H / p->HK);
     const recipe_t rc = recipe_for(p->SK);
@@ -722,7 +729,13 @@ static void emu_item(const void* vctx, long item) {
 void mxo_emulate_ex(const mxo_problem* p, int splits, int rows, uint16_t* out_bf16, void* ohat, float* lse_f32,
                     int f32_partials, int split_tiles, int threads) {
     if (rows <= 0 || rows > p->S) rows = p->S;
-    emu_ctx c = {p, splits, rows, out_bf16, ohat, lse_f32, f32_partials, split_tiles};
+    emu_ctx c = {p, splits, rows, out_bf16, ohat, lse_f32, f32_partials, split_tiles, NULL};
+    run_parallel(threads, (long)p->B * p->H * rows, &c, emu_item);
+}
+
+void mxo_emulate_rows(const mxo_problem* p, int splits, const int* row_list, int rows, uint16_t* out_bf16, int f32_partials,
+                      int split_tiles, int threads) {
+    emu_ctx c = {p, splits, rows, out_bf16, NULL, NULL, f32_partials, split_tiles, row_list};
     run_parallel(threads, (long)p->B * p->H * rows, &c, emu_item);
 }
 

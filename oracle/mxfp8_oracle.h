@@ -93,6 +93,8 @@ void mxo_split_range(int SK, int splits, int s, int* key_lo, int* kv_eff);
 /* fp64 attention check of a bf16 output [B,S,H,128] on the first `rows` query
  * rows of every (b, h) (ref_host.cpp:436-471; scale ln 2). threads <= 0: all cores. */
 mxo_check_result mxo_check_fp64(const mxo_problem* p, const uint16_t* out_bf16, int rows, int threads);
+/* The same over the query rows row_list[0 .. nrows) of every (b, h) (each in [0, S), any order). */
+mxo_check_result mxo_check_fp64_rows(const mxo_problem* p, const uint16_t* out_bf16, const int* row_list, int nrows, int threads);
 
 /* fp32 attention on the dequantised inputs for rows [0, rows) of every (b,h)
  * (rows <= 0: all), result into out_f32 [B,S,H,128] (may be NULL: compute only).
@@ -118,6 +120,9 @@ void mxo_combine(const uint16_t* ohat_f16, const float* lse, uint16_t* out_bf16,
  * mxo_emulate is mxo_emulate_ex(..., 0, 0, ...). */
 void mxo_emulate_ex(const mxo_problem* p, int splits, int rows, uint16_t* out_bf16, void* ohat, float* lse_f32,
                     int f32_partials, int split_tiles, int threads);
+/* mxo_emulate_ex (no partials out) over the query rows row_list[0 .. nrows) of every (b, h). */
+void mxo_emulate_rows(const mxo_problem* p, int splits, const int* row_list, int nrows, uint16_t* out_bf16, int f32_partials,
+                      int split_tiles, int threads);
 void mxo_combine_f32(const float* ohat_f32, const float* lse, uint16_t* out_bf16, long rows_total, int splits);
 
 #ifdef __cplusplus

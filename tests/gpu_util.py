@@ -41,9 +41,11 @@ def run(inp, device, path="auto", splits=None, lse=False, poison=True, partials=
 
 
 def compare_to_emulation(out, emu, inp, rows):
-    """Element statistics of the GPU output against the recipe emulation on the first `rows` rows of every (b,h)."""
-    o = out.reshape(inp.B, inp.S, inp.H, D)[:, :rows]
-    e = emu.reshape(inp.B, inp.S, inp.H, D)[:, :rows]
+    """Element statistics of the GPU output against the recipe emulation on `rows` of every (b,h): the first n rows,
+    or a list of rows."""
+    sel = oracle.row_list(inp.S, rows)
+    o = out.reshape(inp.B, inp.S, inp.H, D)[:, sel]
+    e = emu.reshape(inp.B, inp.S, inp.H, D)[:, sel]
     of = oracle.bf16_to_f32(o).astype(np.float64)
     ef = oracle.bf16_to_f32(e).astype(np.float64)
     diff = np.abs(of - ef)
@@ -71,3 +73,68 @@ def lse_reference(inp, rows):
             m = s.max(1, keepdims=True)
             out[b, h] = (m + np.log(np.exp(s - m).sum(1, keepdims=True)))[:, 0]
     return out
+
+
+def run_direct(inp, device, kernel):
+    """Launches one kernel through its C-ABI launcher (validate first), as a reference-style launcher does:
+    kernel "vs128" (fmha_mxfp8_launch_vs128: the 256-row kernel, 512 threads, grid (ceil(S/256), H, B)), "t128"
+    (fmha_mxfp8_launch_t128: the reference-named 128-row kernel with its 256 threads) or "t128_split_tiles". Returns the
+    bf16 output as uint16 numpy [B*S*H*128] (NaN-poisoned before the launch)."""
+    import ctypes
+    import math
+    from amdgpu_rustdsl_amd import lib
+    q, k, v, qs, ks, vs = upload(inp, device)
+    B, H, HK, S, SK = inp.B, inp.H, inp.HK, inp.S, inp.SK
+    out = torch.empty(B, S, H, D, dtype=torch.bfloat16, device=device)
+    out.view(torch.int16).fill_(0x7fc1)
+    a = lib.fill_args(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), qs.data_ptr(), ks.data_ptr(), vs.data_ptr(),
+                      B, H, HK, S, SK)
+    a.flags = (lib.FLAG_CAUSAL if inp.causal else 0) | (lib.FLAG_V_SEQ32 if inp.vs32 is not None else 0)
+    rows = 256 if kernel == "vs128" else 128
+    grid = (math.ceil(S / rows), H, B)
+    sz = lib.BufferSizes(ops._cap(q), ops._cap(k), ops._cap(v), ops._cap(out), ops._cap(qs), ops._cap(ks), ops._cap(vs), 0, 0)
+    rc, msg = lib.validate("vs128" if kernel == "vs128" else "t128", a, sz, grid, HK=HK)
+    assert rc == 0, msg
+    fn = {"vs128": lib.raw.fmha_mxfp8_launch_vs128, "t128": lib.raw.fmha_mxfp8_launch_t128,
+          "t128_split_tiles": lib.raw.fmha_mxfp8_launch_t128_split_tiles}[kernel]
+    assert fn(ctypes.byref(a), *grid, torch.cuda.current_stream(device).cuda_stream) == 0
+    torch.cuda.synchronize()
+    return out.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+
+
+def _dequant(inp):
+    """float64 dequantised Q [B,S,H,128], K and V [B,SK,HK,128] (V with its descale; the per-tensor descale only)."""
+    dec = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy().astype(np.float64)
+    dec[[0x7F, 0xFF]] = 0.0
+    B, H, HK, S, SK = inp.B, inp.H, inp.HK, inp.S, inp.SK
+    q = dec[inp.q].reshape(B, S, H, 4, 32) * 2.0 ** (inp.qs[: B * S * H * 4].reshape(B, S, H, 4, 1).astype(np.float64) - 127)
+    k = dec[inp.k].reshape(B, SK, HK, 4, 32) * 2.0 ** (inp.ks[: B * SK * HK * 4].reshape(B, SK, HK, 4, 1).astype(np.float64) - 127)
+    v = dec[inp.v].reshape(B, SK, HK, D) * float(inp.vdescale)
+    return q.reshape(B, S, H, D), k.reshape(B, SK, HK, D), v
+
+
+def fp64_rows(inp, rows):
+    """float64 attention of the listed rows (base-2 scores, as ref_host.cpp:436-471 checks them; no causal mask) and,
+    per row, the gap between its two largest scores and the sum of those two keys' score magnitudes sum_d |q_d k_d|
+    (log2 units). Returns (out [B, n, H, 128], gap [B, n, H], mag [B, n, H])."""
+    assert not inp.causal
+    sel = oracle.row_list(inp.S, rows)
+    q, k, v = _dequant(inp)
+    B, H, HK = inp.B, inp.H, inp.HK
+    g = H // HK
+    out = np.zeros((B, sel.size, H, D))
+    gap = np.zeros((B, sel.size, H))
+    mag = np.zeros((B, sel.size, H))
+    for b in range(B):
+        for h in range(H):
+            qs, ks = q[b, sel, h], k[b, :, h // g]
+            s = qs @ ks.T
+            m = np.abs(qs) @ np.abs(ks).T
+            order = np.argsort(-s, axis=1)
+            top = np.take_along_axis(s, order[:, :2], 1) if s.shape[1] > 1 else np.concatenate([s, s - np.inf], 1)
+            gap[b, :, h] = top[:, 0] - top[:, 1]
+            mag[b, :, h] = np.take_along_axis(m, order[:, :1], 1)[:, 0] + (
+                np.take_along_axis(m, order[:, 1:2], 1)[:, 0] if s.shape[1] > 1 else 0.0)
+            w = np.exp2(s - s.max(1, keepdims=True))
+            out[b, :, h] = (w / w.sum(1, keepdims=True)) @ v[b, :, h // g]
+    return out, gap, mag

@@ -57,9 +57,11 @@ def test_parity(gpu, case):
     inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
     out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
     used_splits = used[1] if used[0] == "kvsplit" else 0
-    emu, ref_stats = _emulated_bar(inp, used_splits, path=used[0])
-    stats = oracle.check_fp64(inp, out, rows=ROWS)
-    cmp = gpu_util.compare_to_emulation(out, emu, inp, min(ROWS, S))
+    # the reference's sample (the first 64 rows of every (b, h)) and the last 64: the last query tile and the tail
+    rows = oracle.first_and_last(S, ROWS)
+    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0])
+    stats = oracle.check_fp64(inp, out, rows=rows)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
     print(f"[case] {name} path={used} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
     # every element written (the output was NaN-poisoned), full tensor
     assert not np.isnan(oracle.bf16_to_f32(out)).any(), "unwritten / NaN outputs"
@@ -88,9 +90,9 @@ def test_parity_causal(gpu, case):
     inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=True)
     out, used, _ = gpu_util.run(inp, gpu)
     assert used[0] in ("vs128", "t128")
-    # rows checked: all of them for the small shapes, the first 256 of every (b, h) for cfg4 (its first block,
-    # whose keys are cut by the mask on every tile of the diagonal)
-    rows = S if B * H * S * SK <= (1 << 24) else 256
+    # rows checked: all of them for the small shapes; for cfg4 the first 128 of every (b, h) (the mask cuts every
+    # tile they see) and the last 128 (they see all 16 key tiles: the many-tile lazy rebase under the mask)
+    rows = S if B * H * S * SK <= (1 << 24) else oracle.first_and_last(S, 128)
     emu, ref_stats = _emulated_bar(inp, 0, rows=rows, path=used[0])
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
@@ -155,7 +157,7 @@ def test_parity_v_seq32(gpu, case):
     out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
     assert used[0] == path
     used_splits = used[1] if used[0] == "kvsplit" else 0
-    rows = min(S, 256 if causal else ROWS)
+    rows = oracle.first_and_last(S, 128 if causal else ROWS)
     emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0])
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
@@ -247,7 +249,7 @@ def test_parity_qk_scale(gpu, case):
     out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
     assert used[0] == path
     used_splits = used[1] if used[0] == "kvsplit" else 0
-    rows = S if path == "kvsplit" else min(S, 256 if causal else ROWS)
+    rows = S if path == "kvsplit" else oracle.first_and_last(S, 128 if causal else ROWS)
     emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0])
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
@@ -261,7 +263,7 @@ def test_parity_qk_scale(gpu, case):
 
 # The t128 path's split-tile kernel (extension: 512 threads on t128's 128-row blocks, the two wave groups splitting each
 # tile's keys), on every row: shapes of the reference's t128 dispatch, GQA, a ragged tail, causal, and through the
-# direct launcher (fmha_mxfp8_launch_t128 uses the same kernel).
+# direct launcher fmha_mxfp8_launch_t128_split_tiles.
 T128_ST_CASES = [
     ("B1H8S1024", 1, 8, 8, 1024, 1024, False),
     ("B2H8S512_gqa4", 2, 8, 2, 512, 512, False),
@@ -288,7 +290,7 @@ def test_parity_t128_split_tiles(gpu, case):
     assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
     assert cmp["max_abs"] <= 0.05, cmp
     if not causal:
-        # the direct launcher picks the same kernel (512 threads, t128's grid): bit-identical output
+        # the direct launcher of the same kernel (512 threads, t128's grid): bit-identical output
         import ctypes, math, torch
         from amdgpu_rustdsl_amd import lib
         q, k, v, qs, ks, vs = gpu_util.upload(inp, gpu)
@@ -296,7 +298,7 @@ def test_parity_t128_split_tiles(gpu, case):
         a = lib.fill_args(o2.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), qs.data_ptr(), ks.data_ptr(), vs.data_ptr(),
                           B, H, HK, S, SK)
         st = torch.cuda.current_stream(gpu).cuda_stream
-        assert lib.raw.fmha_mxfp8_launch_t128(ctypes.byref(a), math.ceil(S / 128), H, B, st) == 0
+        assert lib.raw.fmha_mxfp8_launch_t128_split_tiles(ctypes.byref(a), math.ceil(S / 128), H, B, st) == 0
         torch.cuda.synchronize()
         direct = o2.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
         np.testing.assert_array_equal(direct, out)
@@ -322,7 +324,7 @@ def test_parity_vs128_split_tiles(gpu, case):
     inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
     out, used, _ = gpu_util.run(inp, gpu, path=force or "auto")
     assert used[0] == "vs128"
-    rows = min(S, 256)
+    rows = oracle.first_and_last(S, 128)   # the first and the last q tile of every (b, h)
     emu, ref_stats = _emulated_bar(inp, 0, rows=rows, path="vs128")
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
