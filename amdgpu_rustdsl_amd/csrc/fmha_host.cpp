@@ -241,6 +241,7 @@ int fmha_mxfp8_validate_kvsplit(const fmha_mxfp8_kvsplit_args* ka, const fmha_mx
     int rc;
     if ((rc = rules_extent(a, *sz, B, (ka->kvs_splits & FMHA_KVS_V_SEQ32) != 0, err, errlen)) != FMHA_OK) return rc;
     if (sz->ptr_ohat < (uint64_t)(splits * rows * row_bytes)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_ohat: buffer ptr_ohat smaller than declared allocation");
+    if (splits * rows * row_bytes >= (1LL << 32)) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x284) outside contract (partials of 4 GiB or more)");
     if (sz->ptr_lse < (uint64_t)(splits * rows * 4)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_lse: buffer ptr_lse smaller than declared allocation");
     if ((rc = rules_range(a, err, errlen)) != FMHA_OK) return rc;
     if (splits < 1 || (ka->kvs_splits & ~(0xffffu | FMHA_KVS_F32_PARTIALS | FMHA_KVS_V_SEQ32 | FMHA_KVS_SCALE)) != 0)
@@ -262,6 +263,7 @@ int fmha_mxfp8_validate_combine(const fmha_mxfp8_combine_args* a, const fmha_mxf
     const i64 rows = a->rows_total, splits = a->splits & 0xffffu;
     if (sz->ptr_ohat < (uint64_t)(splits * rows * 512)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_ohat: buffer ptr_ohat smaller than declared allocation");
     if (sz->ptr_lse < (uint64_t)(splits * rows * 4)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_lse: buffer ptr_lse smaller than declared allocation");
+    if (splits * rows * 512 >= (1LL << 32)) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x18) outside contract (partials of 4 GiB or more)");
     if (sz->ptr_o < (uint64_t)(rows * 256)) return fail(err, errlen, FMHA_ERR_EXTENT, "GV-HOST-EXTENT", "ptr_out: buffer ptr_out smaller than declared allocation");
     if (rows < 1) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x18) outside contract");
     if (a->d != 128) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x1C) outside contract");

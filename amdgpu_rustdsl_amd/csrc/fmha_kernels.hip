@@ -832,6 +832,89 @@ struct Wave {
 // The row sum of this lane's query (the ones pattern puts it in D dword (lane / 16) % 2).
 __device__ __forceinline__ float row_sum(const v4f& lacc, uint32_t lane) { return ((lane >> 4) & 1u) ? lacc[1] : lacc[0]; }
 
+// The LSE-weighted merge of the splits' partial rows (epilogue.rs:89-167) for NG groups: group t[g] is outputs
+// 8 (t & 15) .. +7 of partial row t >> 4, merged over splits 0 .. splits - 1 in order; out[g] receives the 8 bf16
+// results. F32: f32 partial rows (the extension) instead of fp16. For up to 8 splits every load of the NG groups is
+// issued before the first merge step, in one straight-line block with no branch: one memory latency per call (with a
+// branch per split on the row format, the compiler waited for each split's loads in turn).
+template <bool F32, int NG>
+__device__ __forceinline__ void combine_groups(const float* lse, const uint8_t* ohat, uint32_t rows, uint32_t splits,
+                                               const uint32_t (&t)[NG], v4i (&out)[NG]) {
+    constexpr int NW = F32 ? 8 : 4;      // dwords of one split's 8 values
+    // byte offsets below 2^32: validate refuses split partials of 4 GiB or more
+    const __amdgpu_buffer_rsrc_t rl = make_rsrc(lse, 0xffffffffu), ro = make_rsrc(ohat, 0xffffffffu);
+    auto load = [&](uint32_t s, uint32_t tg, uint32_t& l, uint32_t (&xw)[NW]) {
+        const uint32_t r = s * rows + (tg >> 4);   // partial row index
+        l = __builtin_amdgcn_raw_buffer_load_b32(rl, r * 4u, 0, 0);
+        const uint32_t off = ((r << 4) | (tg & 15u)) * (F32 ? 32u : 16u);
+        const v4i x0 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, 0));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xw[i] = (uint32_t)x0[i];
+        if (F32) {
+            const v4i x1 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ro, off + 16u, 0, 0));
+#pragma unroll
+            for (int i = 0; i < NW - 4; ++i) xw[4 + i] = (uint32_t)x1[i];
+        }
+    };
+    struct St {
+        float m, den, acc[8];
+    };
+    auto merge = [](St& st, float l, const uint32_t (&xw)[NW]) {
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            if (F32) x[i] = __builtin_bit_cast(float, xw[i]);
+            else { x[2 * i] = h2f(xw[i]); x[2 * i + 1] = h2f(xw[i] >> 16); }
+        }
+        const float m_new = fmaxf(st.m, l);
+        const float dm = m_new * -1.0f;
+        const float al = __builtin_amdgcn_exp2f(st.m + dm);
+        const float w = __builtin_amdgcn_exp2f(l + dm);
+        st.den = st.den * al + w;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st.acc[i] = st.acc[i] * al + w * x[i];
+        st.m = m_new;
+    };
+    St st[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        st[g].m = -1.0e30f;
+        st[g].den = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st[g].acc[i] = 0.0f;
+    }
+    if (splits <= 8u) {
+        // indices past the split count re-read the last split, which is not merged
+        uint32_t l[NG][8], xw[NG][8][NW];
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (uint32_t s = 0; s < 8u; ++s) load(min(s, splits - 1u), t[g], l[g][s], xw[g][s]);
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (uint32_t s = 0; s < 8u; ++s)
+                if (s < splits) merge(st[g], __builtin_bit_cast(float, l[g][s]), xw[g][s]);
+    } else {
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+            for (uint32_t s = 0; s < splits; ++s) {
+                uint32_t l, xw[NW];
+                load(s, t[g], l, xw);
+                merge(st[g], __builtin_bit_cast(float, l), xw);
+            }
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const float rd = __builtin_amdgcn_rcpf(st[g].den);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const v2bf w = {(__bf16)(st[g].acc[2 * i] * rd), (__bf16)(st[g].acc[2 * i + 1] * rd)};
+            out[g][i] = __builtin_bit_cast(int, w);
+        }
+    }
+}
+
 // Epilogue. Full-sequence kernels: O = O^T . (v_descale / l) -> bf16 rows (state.rs:79-83); the optional natural-log
 // LSE. KV split: the fp16 partial O-hat = (O / 16) (v_descale / l_total) with l_total = l / 16 and
 // lse = log2(l_total) - 2048 (hi + lo) (block3.rs:291-356, softmax.rs:308-322), partial row
@@ -1408,65 +1491,14 @@ extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvspli
     (void)a_;
     const uint32_t rows = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, rows_total));
     const uint32_t split_field = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, splits));
-    const uint32_t splits = split_field & 0xffffu;
-    const bool f32 = (split_field & FMHA_KVS_F32_PARTIALS) != 0u;   // extension: f32 partial rows
     const uint32_t groups = rows << 4;
     uint32_t t = blockIdx.x * 256u + threadIdx.x;
     t = t < groups ? t : groups - 1u;
-    const uint32_t row = t >> 4;
     const float* lse = (const float*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_lse));
     const uint8_t* ohat = (const uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_ohat));
-    float m = -1.0e30f, den = 0.0f;
-    float acc[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    // split s's LSE and 8 partial values of this thread
-    auto load = [&](uint32_t s, float& l, float (&x)[8]) {
-        const size_t rs = (size_t)s * rows;
-        l = lse[rs + row];
-        if (f32) {
-            const v4f x0 = *(const v4f*)(ohat + ((rs << 4) + t) * 32u), x1 = *(const v4f*)(ohat + ((rs << 4) + t) * 32u + 16u);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { x[i] = x0[i]; x[4 + i] = x1[i]; }
-        } else {
-            const v4i ov = *(const v4i*)(ohat + ((rs << 4) + t) * 16u);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { x[2 * i] = h2f((uint32_t)ov[i]); x[2 * i + 1] = h2f((uint32_t)ov[i] >> 16); }
-        }
-    };
-    // the streaming LSE-weighted merge (epilogue.rs:89-167), split by split in order
-    auto merge = [&](float l, const float (&x)[8]) {
-        const float m_new = fmaxf(m, l);
-        const float dm = m_new * -1.0f;
-        const float al = __builtin_amdgcn_exp2f(m + dm);
-        const float w = __builtin_amdgcn_exp2f(l + dm);
-        den = den * al + w;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = acc[i] * al + w * x[i];
-        m = m_new;
-    };
-    if (splits <= 8u) {
-        // every split's loads issued before the first merge: one memory latency instead of one per split (indices past
-        // the split count re-read the last split, which is not merged)
-        float l[8], x[8][8];
-#pragma unroll
-        for (uint32_t s = 0; s < 8u; ++s) load(min(s, splits - 1u), l[s], x[s]);
-#pragma unroll
-        for (uint32_t s = 0; s < 8u; ++s)
-            if (s < splits) merge(l[s], x[s]);
-    } else {
-        for (uint32_t s = 0; s < splits; ++s) {
-            float l, x[8];
-            load(s, l, x);
-            merge(l, x);
-        }
-    }
-    const float rd = __builtin_amdgcn_rcpf(den);
-    v4i outv;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const v2bf w = {(__bf16)(acc[2 * i] * rd), (__bf16)(acc[2 * i + 1] * rd)};
-        outv[i] = __builtin_bit_cast(int, w);
-    }
-    *(v4i*)((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u) = outv;
+    const uint32_t tg[1] = {t};
+    v4i outv[1];
+    if (split_field & FMHA_KVS_F32_PARTIALS) combine_groups<true, 1>(lse, ohat, rows, split_field & 0xffffu, tg, outv);
+    else combine_groups<false, 1>(lse, ohat, rows, split_field & 0xffffu, tg, outv);
+    *(v4i*)((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u) = outv[0];
 }
