@@ -11,12 +11,13 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <atomic>
 
 #include "../../include/fmha_mxfp8.h"
 #include "module_cache.h"
 
 static_assert(sizeof(fmha_mxfp8_args) == 656, "kernarg size (vs128_abi.h:126)");
-static_assert(sizeof(fmha_mxfp8_params) == 168, "params layout (lib.py mirrors it)");
+static_assert(sizeof(fmha_mxfp8_params) == 176, "params layout (lib.py mirrors it)");
 static_assert(offsetof(fmha_mxfp8_args, ptr_o) == 0x000, "ptr_o");
 static_assert(offsetof(fmha_mxfp8_args, ptr_q) == 0x010, "ptr_q");
 static_assert(offsetof(fmha_mxfp8_args, ptr_k) == 0x020, "ptr_k");
@@ -105,8 +106,9 @@ int t128_kernel(uint32_t SK, bool scaled, uint32_t* block) {
 // The one-call entry also runs the vs128 path on the split-tile kernel when its 256-row grid holds at most 128
 // blocks (half of the 256 CUs or fewer): on t128's 128-row grid the same shape fills twice the CUs. Not with the LUT
 // recipe (fewer than 4 key tiles), as for t128. The direct vs128 launcher keeps the 256-row kernel its grid names.
-bool vs128_split_tiles(int64_t B, int64_t H, int64_t S, int64_t SK) {
-    return (S + 255) / 256 * H * B <= 128 && t128_split_tiles(SK);
+// Causal (extension): always, so that the 128-row grid's causal q-tile pairing is available past one wave of blocks.
+bool vs128_split_tiles(int64_t B, int64_t H, int64_t S, int64_t SK, bool causal) {
+    return (causal || (S + 255) / 256 * H * B <= 128) && t128_split_tiles(SK);
 }
 
 fmha_internal::ModuleCache<9> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
@@ -171,9 +173,23 @@ int rules_is(const fmha_mxfp8_args& a, i64 HK, char* err, size_t errlen) {
 
 int rules_grid(const fmha_mxfp8_args& a, uint32_t gx, uint32_t gy, int rows_per_block, char* err, size_t errlen) {
     if ((i64)gy != (i64)a.s_q_head_num) return fail(err, errlen, FMHA_ERR_GRID, "GV-HOST-GRID", "grid axis 1 relation failed");
-    if ((i64)gx != ((i64)a.s_seq_len + rows_per_block - 1) / rows_per_block)
-        return fail(err, errlen, FMHA_ERR_GRID, "GV-HOST-GRID", "grid axis 0 relation failed");
+    i64 want = ((i64)a.s_seq_len + rows_per_block - 1) / rows_per_block;
+    if (a.flags & FMHA_FLAG_CAUSAL_PAIR) want = (want + 1) / 2;   // the causal q-tile pairing: two tiles per block
+    if ((i64)gx != want) return fail(err, errlen, FMHA_ERR_GRID, "GV-HOST-GRID", "grid axis 0 relation failed");
     return FMHA_OK;
+}
+
+// Compute units of the current device (the causal pairing pays off only when the unpaired grid exceeds them), cached
+int cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
 // The in-kernel softmax scale (FMHA_FLAG_SCALE / FMHA_KVS_SCALE): c = f32(scale log2 e) must be a positive normal f32
@@ -195,7 +211,8 @@ int validate_base(const fmha_mxfp8_args& a, const fmha_mxfp8_buffer_sizes& sz, u
     int rc;
     if ((rc = rules_extent(a, sz, B, (a.flags & FMHA_FLAG_V_SEQ32) != 0, err, errlen)) != FMHA_OK) return rc;
     if ((rc = rules_range(a, err, errlen)) != FMHA_OK) return rc;
-    if ((a.flags & ~(FMHA_FLAG_CAUSAL | FMHA_FLAG_V_SEQ32 | FMHA_FLAG_SCALE)) != 0)
+    if ((a.flags & ~(FMHA_FLAG_CAUSAL | FMHA_FLAG_V_SEQ32 | FMHA_FLAG_SCALE | FMHA_FLAG_CAUSAL_PAIR)) != 0 ||
+        ((a.flags & FMHA_FLAG_CAUSAL_PAIR) && !(a.flags & FMHA_FLAG_CAUSAL)))
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x280) outside contract");
     if ((rc = rules_scale(a, (a.flags & FMHA_FLAG_SCALE) != 0, err, errlen)) != FMHA_OK) return rc;
     if ((rc = rules_is(a, HK, err, errlen)) != FMHA_OK) return rc;
@@ -221,6 +238,8 @@ int fmha_mxfp8_init(char* err, size_t errlen) {
 
 int fmha_mxfp8_validate_vs128(const fmha_mxfp8_args* a, const fmha_mxfp8_buffer_sizes* sz, uint32_t gx, uint32_t gy,
                               uint32_t gz, int64_t HK, char* err, size_t errlen) {
+    // the causal q-tile pairing runs on the 128-row grid only
+    if (a->flags & FMHA_FLAG_CAUSAL_PAIR) return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x280) outside contract");
     return validate_base(*a, *sz, gx, gy, (i64)gz, HK, 256, err, errlen);
 }
 
@@ -272,9 +291,9 @@ int fmha_mxfp8_validate_combine(const fmha_mxfp8_combine_args* a, const fmha_mxf
     return FMHA_OK;
 }
 
-int fmha_mxfp8_uses_split_tiles(int path, int64_t B, int64_t H, int64_t S, int64_t SK) {
+int fmha_mxfp8_uses_split_tiles(int path, int64_t B, int64_t H, int64_t S, int64_t SK, int causal) {
     if (path == FMHA_PATH_T128) return t128_split_tiles(SK) ? 1 : 0;
-    if (path == FMHA_PATH_VS128) return vs128_split_tiles(B, H, S, SK) ? 1 : 0;
+    if (path == FMHA_PATH_VS128) return vs128_split_tiles(B, H, S, SK, causal != 0) ? 1 : 0;
     return 0;
 }
 
@@ -380,6 +399,8 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "f32_partials must be 0 or 1");
     if (p->v_seq32 != 0 && p->v_seq32 != 1)
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "v_seq32 must be 0 or 1");
+    if (p->causal_pair < 0 || p->causal_pair > 2)
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "causal_pair must be 0, 1 or 2");
     const bool scaled = p->softmax_scale != 0.0f;
     if (scaled && !scale_ok(p->softmax_scale))
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "softmax_scale must be 0 or positive with a normal f32 scale x log2(e)");
@@ -407,11 +428,19 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
         int kern;
         if (path == FMHA_PATH_T128) {
             kern = t128_kernel((uint32_t)SK, scaled, &block);
-        } else if (vs128_split_tiles(B, H, S, SK)) {
+        } else if (vs128_split_tiles(B, H, S, SK, p->causal != 0)) {
             kern = scaled ? K_T128ST_SC : K_T128ST;   // same kernarg layout, 128-row grid
             kgx = (uint32_t)((S + 127) / 128);
         } else {
             kern = scaled ? K_VS128_SC : K_VS128;
+        }
+        // the causal q-tile pairing when the grid would take more than one wave of blocks (the extension's flag; the
+        // reference pairs its causal kernels' tiles always, grid.rs:94-111), or when the caller asks for it
+        const bool pair = p->causal && kern != K_VS128 && kern != K_VS128_SC && kgx > 1 &&
+                          (p->causal_pair == 1 || (p->causal_pair == 0 && (i64)kgx * H * B > (i64)cu_count()));
+        if (pair) {
+            a.flags |= FMHA_FLAG_CAUSAL_PAIR;
+            kgx = (kgx + 1) / 2;
         }
         return launch_raw(kern, &a, sizeof(a), kgx, gy, (uint32_t)B, block, stream, err, errlen);
     }

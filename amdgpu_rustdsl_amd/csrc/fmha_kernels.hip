@@ -210,10 +210,13 @@ __device__ inline uint32_t slot_base(uint32_t lds, uint32_t region, uint32_t slo
 }
 
 // uniform base + per-lane offset as one opaque VGPR: constant offsets added to it afterwards fold into the LDS
-// instruction's immediate (left to itself the compiler reassociates base + constant first, one add per read)
+// instruction's immediate (left to itself the compiler reassociates base + constant first, one add per read).
+// The add is the compiler's own and the empty asm only hides its value: a VGPR written by an instruction inside
+// inline asm is outside the compiler's hazard checks, and a register whose MFMA result is dead but still in flight
+// (the row-sum MFMA's unused dwords) can be handed to it and overwritten by the MFMA's late write.
 __device__ inline uint32_t lane_addr(uint32_t uniform_base, uint32_t lane_off) {
-    uint32_t r;
-    asm("v_add_u32 %0, %1, %2" : "=v"(r) : "s"(uniform_base), "v"(lane_off));
+    uint32_t r = uniform_base + lane_off;
+    asm("" : "+v"(r));
     return r;
 }
 
@@ -263,7 +266,7 @@ __device__ inline void lds_write4(uint32_t off, uint32_t v) { *(LDS_AS uint32_t*
 // explicit instead: a copy is published by the barrier that follows the wait on its vmcnt (block_barrier_keep_dma).
 // M0 carries the LDS base; no compiler-generated code in these kernels uses M0.
 __device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :
                  : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
                  : "memory");
@@ -271,7 +274,7 @@ __device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uin
 
 // The same with 4 bytes per lane: lane L's bytes land at lds_base + 4 L.
 __device__ inline void dma4(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
                  :
                  : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
                  : "memory");
@@ -681,8 +684,8 @@ struct Wave {
     // The ones operand of the row-sum MFMA, rebuilt where it is used (an opaque copy, so the compiler neither keeps
     // it live across the loop nor hoists it: 8 VGPRs only around the row-sum MFMAs).
     __device__ __forceinline__ v8i ones_op() const {
-        uint32_t x;
-        asm volatile("v_mov_b32 %0, %1" : "=v"(x) : "v"(onew));
+        uint32_t x = onew;
+        asm volatile("" : "+v"(x));   // a copy the compiler makes (and hazard-checks), as in lane_addr
         return __builtin_bit_cast(v8i, splat8(__builtin_bit_cast(float, x)));
     }
     __device__ __forceinline__ v16f qk_mfma(const v8i& kf, const v8i& qf, const v16f& c_in, uint32_t ksw, int c) const {
@@ -927,8 +930,9 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
                                          bool sync) {
     // lane-derived values recomputed here from an opaque lane id: kept from the prologue they would be live (and
     // spilled) across the whole loop
-    uint32_t lane;
-    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+    uint32_t all = ~0u;
+    asm volatile("" : "+s"(all));   // an opaque mask, so the lane index is computed here (see lane_addr on inline asm)
+    const uint32_t lane = __builtin_amdgcn_mbcnt_hi(all, __builtin_amdgcn_mbcnt_lo(all, 0u));
     const uint32_t hh = lane >> 5, n = lane & 31u, row = w.row0 + n;
     const float l = row_sum(w.lacc, lane);
     const uint32_t dbase = 4u * hh;
@@ -1197,10 +1201,9 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     }
     FMHA_MARK(p, tblk, 4);
     FMHA_LFLUSH(p, tblk);
-    if (HV) {
-        if (!merge_halves<GB>(w, lds)) return;   // B's state is in A's now
-    }
-    epilogue<SPLIT>(p, w, head, bidx, split, rc, !HV);   // HV: the merge's barriers already retired the ring
+    // HV: B's state is in A's now, and only A writes (B goes on to the end: the causal pairing's second pass follows
+    // a block barrier)
+    if (!HV || merge_halves<GB>(w, lds)) epilogue<SPLIT>(p, w, head, bidx, split, rc, !HV);   // HV: the merge's barriers retired the ring
     FMHA_MARK(p, tblk, 5);
 }
 
@@ -1315,8 +1318,10 @@ __device__ __forceinline__ void attend_pipelined(const Prm& p, uint32_t lds, uin
 // gives XCD k the slice's logical blocks [k n / 8, (k + 1) n / 8). The grid extents come from the kernel arguments
 // (gx = ceil(S / rows), gy = H): reading them from the dispatch packet, which sits in the host-memory queue, cost every
 // wave a round trip over PCIe at start-up (microseconds, growing with the wave count).
-__device__ inline void block_coords(uint32_t S, uint32_t H, uint32_t rows, uint32_t& qt, uint32_t& head, uint32_t& z) {
-    const uint32_t gx = (S + rows - 1u) / rows;
+// pair: the causal q-tile pairing (FMHA_FLAG_CAUSAL_PAIR): the grid's x extent is ceil(T / 2) for T query tiles.
+__device__ inline void block_coords(uint32_t S, uint32_t H, uint32_t rows, uint32_t& qt, uint32_t& head, uint32_t& z, bool pair = false) {
+    const uint32_t nt = (S + rows - 1u) / rows;
+    const uint32_t gx = pair ? (nt + 1u) / 2u : nt;
     const uint32_t n = gx * H;
     uint32_t L = blockIdx.x + gx * blockIdx.y;
     if ((n & 7u) == 0u) L = (L & 7u) * (n >> 3) + (L >> 3);
@@ -1337,10 +1342,10 @@ __device__ __forceinline__ void full_kernel(uint32_t lds) {
 #else
     const Prm p = prm_from_kernarg<SC>();
 #endif
-    uint32_t qt, head, z;
-    block_coords(p.S, p.H, NT / 2, qt, head, z);
     const bool lut = (p.SK + 127u) / 128u < 4u;   // state.rs:75-77
-    if (NT == 512) {
+    if constexpr (NT == 512) {
+        uint32_t qt, head, z;
+        block_coords(p.S, p.H, 256u, qt, head, z);
         if (p.vs32) {
             if (lut) attend_pingpong<true, false, true, false, SC>(p, lds, qt, head, z, 0, 0, p.SK);
             else attend_pingpong<false, false, true, false, SC>(p, lds, qt, head, z, 0, 0, p.SK);
@@ -1349,12 +1354,24 @@ __device__ __forceinline__ void full_kernel(uint32_t lds) {
             else attend_pingpong<false, false, false, false, SC>(p, lds, qt, head, z, 0, 0, p.SK);
         }
     } else {
-        if (p.vs32) {
-            if (lut) attend_pipelined<true, true, SC>(p, lds, qt, head, z, 0, p.SK);
-            else attend_pipelined<false, true, SC>(p, lds, qt, head, z, 0, p.SK);
-        } else {
-            if (lut) attend_pipelined<true, false, SC>(p, lds, qt, head, z, 0, p.SK);
-            else attend_pipelined<false, false, SC>(p, lds, qt, head, z, 0, p.SK);
+        // the causal q-tile pairing (FMHA_FLAG_CAUSAL_PAIR, 128-row grids only: the 256-row kernel's registers have no
+        // room for the pass loop, and validate refuses the flag for it; grid.rs:94-111): block x runs q tiles x and
+        // T - 1 - x (the second only when it is past x), so every block does the same work; a barrier between passes
+        uint32_t x, head, z;
+        const bool pair = (p.flags & FMHA_FLAG_CAUSAL_PAIR) != 0u;
+        block_coords(p.S, p.H, 128u, x, head, z, pair);
+        const uint32_t nt = (p.S + 127u) / 128u;
+        const uint32_t npass = pair && nt - 1u - x > x ? 2u : 1u;
+        for (uint32_t pass = 0; pass < npass; ++pass) {
+            const uint32_t qt = pass == 0u ? x : nt - 1u - x;
+            if (pass > 0u) block_barrier();
+            if (p.vs32) {
+                if (lut) attend_pipelined<true, true, SC>(p, lds, qt, head, z, 0, p.SK);
+                else attend_pipelined<false, true, SC>(p, lds, qt, head, z, 0, p.SK);
+            } else {
+                if (lut) attend_pipelined<true, false, SC>(p, lds, qt, head, z, 0, p.SK);
+                else attend_pipelined<false, false, SC>(p, lds, qt, head, z, 0, p.SK);
+            }
         }
     }
 }
@@ -1416,15 +1433,22 @@ __device__ __forceinline__ void t128_split_tiles_kernel(uint32_t lds) {
 #else
     const Prm p = prm_from_kernarg<SC>();
 #endif
-    uint32_t qt, head, z;
-    block_coords(p.S, p.H, 128u, qt, head, z);
+    uint32_t x, head, z;
+    const bool pair = (p.flags & FMHA_FLAG_CAUSAL_PAIR) != 0u;
+    block_coords(p.S, p.H, 128u, x, head, z, pair);
     const bool lut = (p.SK + 127u) / 128u < 4u;   // state.rs:75-77
-    if (p.vs32) {
-        if (lut) attend_pingpong<true, false, true, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
-        else attend_pingpong<false, false, true, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
-    } else {
-        if (lut) attend_pingpong<true, false, false, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
-        else attend_pingpong<false, false, false, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
+    const uint32_t nt = (p.S + 127u) / 128u;
+    const uint32_t npass = pair && nt - 1u - x > x ? 2u : 1u;   // the causal q-tile pairing, as in full_kernel
+    for (uint32_t pass = 0; pass < npass; ++pass) {
+        const uint32_t qt = pass == 0u ? x : nt - 1u - x;
+        if (pass > 0u) block_barrier();
+        if (p.vs32) {
+            if (lut) attend_pingpong<true, false, true, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
+            else attend_pingpong<false, false, true, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
+        } else {
+            if (lut) attend_pingpong<true, false, false, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
+            else attend_pingpong<false, false, false, true, SC>(p, lds, qt, head, z, 0, 0, p.SK);
+        }
     }
 }
 

@@ -28,7 +28,7 @@ PATH_VS128, PATH_T128, PATH_KVSPLIT = 0, 1, 2
 KVS_F32_PARTIALS = 0x10000   # include/fmha_mxfp8.h FMHA_KVS_F32_PARTIALS
 KVS_V_SEQ32 = 0x20000        # FMHA_KVS_V_SEQ32
 KVS_SCALE = 0x40000          # FMHA_KVS_SCALE
-FLAG_CAUSAL, FLAG_V_SEQ32, FLAG_SCALE = 0x1, 0x2, 0x4   # FMHA_FLAG_*
+FLAG_CAUSAL, FLAG_V_SEQ32, FLAG_SCALE, FLAG_CAUSAL_PAIR = 0x1, 0x2, 0x4, 0x8   # FMHA_FLAG_*
 PATH_NAMES = {PATH_VS128: "vs128", PATH_T128: "t128", PATH_KVSPLIT: "kvsplit"}
 PATH_IDS = {v: k for k, v in PATH_NAMES.items()}
 
@@ -80,10 +80,10 @@ class Params(ctypes.Structure):
                 ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("HK", ctypes.c_int32), ("S", ctypes.c_int32), ("SK", ctypes.c_int32),
                 ("path", ctypes.c_int32), ("splits", ctypes.c_int32), ("causal", ctypes.c_int32),
                 ("f32_partials", ctypes.c_int32), ("v_seq32", ctypes.c_int32), ("softmax_scale", ctypes.c_float),
-                ("no_check", ctypes.c_int32)]
+                ("no_check", ctypes.c_int32), ("causal_pair", ctypes.c_int32)]
 
 
-assert ctypes.sizeof(Params) == 168 and ctypes.sizeof(Args) == 656 and ctypes.sizeof(KvsplitArgs) == 648 and ctypes.sizeof(CombineArgs) == 36
+assert ctypes.sizeof(Params) == 176 and ctypes.sizeof(Args) == 656 and ctypes.sizeof(KvsplitArgs) == 648 and ctypes.sizeof(CombineArgs) == 36
 
 _c, _i64, _sz, _cp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_char_p
 _P = ctypes.POINTER
@@ -92,7 +92,7 @@ _L.fmha_mxfp8_validate_t128.argtypes = [_P(Args), _P(BufferSizes), _u32, _u32, _
 _L.fmha_mxfp8_validate_kvsplit.argtypes = [_P(KvsplitArgs), _P(BufferSizes), _u32, _u32, _u32, _i64, _i64, _i64, _cp, _sz]
 _L.fmha_mxfp8_validate_combine.argtypes = [_P(CombineArgs), _P(BufferSizes), _u32, _u32, _u32, _cp, _sz]
 _L.fmha_mxfp8_select_path.argtypes = [_i64, _i64, _i64, _i64, _P(_c)]
-_L.fmha_mxfp8_uses_split_tiles.argtypes = [_c, _i64, _i64, _i64, _i64]
+_L.fmha_mxfp8_uses_split_tiles.argtypes = [_c, _i64, _i64, _i64, _i64, _c]
 _L.fmha_mxfp8_fill_args.argtypes = [_P(Args), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c, _c, _c, _c, _c]
 _L.fmha_mxfp8_fill_args.restype = None
 _L.fmha_mxfp8_workspace_bytes.argtypes = [_i64, _i64, _i64, _c]
@@ -145,11 +145,11 @@ def select_path(B, H, S, SK):
     return PATH_NAMES[path], sp.value
 
 
-def uses_split_tiles(path, B, H, S, SK):
+def uses_split_tiles(path, B, H, S, SK, causal=False):
     """Whether the one-call entry runs the full-sequence `path` ("vs128" / "t128") on the split-tile kernel."""
     if path not in ("vs128", "t128"):
         return False
-    return bool(_L.fmha_mxfp8_uses_split_tiles(PATH_IDS[path], B, H, S, SK))
+    return bool(_L.fmha_mxfp8_uses_split_tiles(PATH_IDS[path], B, H, S, SK, int(bool(causal))))
 
 
 def workspace_bytes(B, H, S, splits):

@@ -53,7 +53,7 @@ def _ws(device, stream, nbytes):
 
 
 def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", splits=None, specialize=True, stream=None, check=True,
-                   lse=None, causal=False, partials="fp16", softmax_scale=None):
+                   lse=None, causal=False, partials="fp16", softmax_scale=None, causal_pair="auto"):
     """Attention forward on MXFP8 inputs with head dim 128, written into ``out``; returns the (path, splits) that ran.
 
     Scores are base-2: the kernels compute softmax2(q . k) over dequantised q and k, so a caller that wants the usual
@@ -73,8 +73,13 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     grid) before the launch; the op's own shape checks still run.
     Extensions: ``lse`` (float32 [B, H, S]) receives the natural-log log-sum-exp of each query row (vs128 / t128);
     ``causal`` masks key t from query i unless t <= i + SK - S; ``partials="fp32"`` keeps the KV split's partial rows
-    in float32; ``softmax_scale`` makes the kernel apply scale * log2(e) to q . k itself (q then quantised unscaled).
+    in float32; ``softmax_scale`` makes the kernel apply scale * log2(e) to q . k itself (q then quantised unscaled);
+    ``causal_pair`` ("auto", True, False): with ``causal``, one block runs query tiles x and T - 1 - x, so that every block
+    has the same work; "auto" pairs when the unpaired grid exceeds the device's CUs (same output bits either way).
     """
+    pair_modes = {"auto": 0, True: 1, False: 2}
+    if causal_pair not in pair_modes:
+        raise ValueError(f"fmha_fwd_mxfp8: causal_pair must be 'auto', True or False, got {causal_pair!r}")
     if partials not in ("fp16", "fp32"):
         raise ValueError(f"fmha_fwd_mxfp8: partials must be 'fp16' or 'fp32', got {partials!r}")
     B, S, H, d = q.shape
@@ -117,6 +122,7 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     p.f32_partials = int(partials == "fp32")
     p.v_seq32 = int(v_seq32)
     p.no_check = int(not check)
+    p.causal_pair = pair_modes[causal_pair]
     if softmax_scale is not None:
         if not float(softmax_scale) > 0.0:
             raise ValueError(f"fmha_fwd_mxfp8: softmax_scale must be positive, got {softmax_scale!r}")

@@ -316,7 +316,7 @@ def kernel_launcher(lib, q, k, v, qs, ks, vs, out, lse, used, B, H, HK, S, SK, c
     path, nsplit = used
     kernel = "fmha_fwd_hd128_mxfp8_v3_" + path
     if path in ("vs128", "t128"):
-        split_tiles = lib.uses_split_tiles(path, B, H, S, SK)
+        split_tiles = lib.uses_split_tiles(path, B, H, S, SK, causal)
         # the kernel the one-call entry runs: the split-tile kernel (t128's grid, 512 threads) or the path's own
         on_t128 = path == "t128" or split_tiles
         grid = (math.ceil(S / (128 if on_t128 else 256)), H, B)

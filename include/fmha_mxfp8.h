@@ -147,6 +147,11 @@ typedef struct fmha_mxfp8_combine_args {
 #define FMHA_FLAG_CAUSAL 0x1u
 #define FMHA_FLAG_V_SEQ32 0x2u
 #define FMHA_FLAG_SCALE 0x4u
+/* With FMHA_FLAG_CAUSAL: the causal q-tile pairing of the reference's causal kernels
+ * (crates/amdgpu-stage/src/templates/grid.rs:94-111, causal_pair): block x runs query tiles x and T - 1 - x (the
+ * second only when it is past x), T = ceil(S / rows), so every block does the same work; grid.x = ceil(T / 2).
+ * The output is bit-identical to the unpaired launch (each tile is computed the same way). */
+#define FMHA_FLAG_CAUSAL_PAIR 0x8u
 #define FMHA_KVS_V_SEQ32 0x20000u
 #define FMHA_KVS_SCALE 0x40000u
 
@@ -204,9 +209,10 @@ int fmha_mxfp8_select_path(int64_t B, int64_t H, int64_t S, int64_t SK, int* spl
 /* Extension (no counterpart in the reference): 1 if fmha_fwd_hd128_mxfp8_auto runs the full-sequence `path`
  * (FMHA_PATH_VS128 or FMHA_PATH_T128) on the split-tile kernel fmha_fwd_hd128_mxfp8_v3_t128_split_tiles (128-row
  * blocks of 512 threads, the two wave groups splitting each tile's keys and merging at the end), else 0. t128: at
- * least 4 key tiles. vs128: also a 256-row grid of at most 128 blocks. The split-tile order rounds differently from
- * the reference's single stream per row; the path and its recipe are the reference's. */
-int fmha_mxfp8_uses_split_tiles(int path, int64_t B, int64_t H, int64_t S, int64_t SK);
+ * least 4 key tiles. vs128: also a 256-row grid of at most 128 blocks, or `causal` (the 128-row grid's causal
+ * q-tile pairing). The split-tile order rounds differently from the reference's single stream per row; the path and
+ * its recipe are the reference's. */
+int fmha_mxfp8_uses_split_tiles(int path, int64_t B, int64_t H, int64_t S, int64_t SK, int causal);
 
 /* Fill the kernarg fields derived from a packed [B,S,H,128] / [B,SK,HK,128]
  * layout (the values ref_host.cpp:342-360 and ops.py:114-118 write). */
@@ -254,6 +260,8 @@ typedef struct fmha_mxfp8_params {
     int32_t no_check;          /* 0 = run the validate rules before launching (the default); 1 = skip them, as the
                                   reference op's check=False does (python/amdgpu_jit/ops.py:88): the caller then
                                   vouches for the buffer extents and strides */
+    int32_t causal_pair;       /* causal only (extension): 0 = the causal q-tile pairing (FMHA_FLAG_CAUSAL_PAIR) when
+                                  the unpaired grid has more blocks than the device has CUs; 1 = always; 2 = never */
 } fmha_mxfp8_params;
 
 /* fmha_fwd_hd128_mxfp8_auto: dispatch + validate + launch (+ combine), all on

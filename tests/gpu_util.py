@@ -26,7 +26,7 @@ def upload(inp, device):
     return q, k, v, qs, ks, vs
 
 
-def run(inp, device, path="auto", splits=None, lse=False, poison=True, partials="fp16"):
+def run(inp, device, path="auto", splits=None, lse=False, poison=True, partials="fp16", causal_pair="auto"):
     """Runs the op; returns (bf16 output as uint16 numpy [B*S*H*128], (path, splits), lse tensor or None)."""
     q, k, v, qs, ks, vs = upload(inp, device)
     out = torch.empty(inp.B, inp.S, inp.H, D, dtype=torch.bfloat16, device=device)
@@ -34,7 +34,8 @@ def run(inp, device, path="auto", splits=None, lse=False, poison=True, partials=
         out.view(torch.int16).fill_(0x7fc1)   # NaN: every element must be written
     lse_t = torch.full((inp.B, inp.H, inp.S), float("nan"), dtype=torch.float32, device=device) if lse else None
     used = ops.fmha_fwd_mxfp8(q, k, v, qs, ks, vs, out, path=path, splits=splits, lse=lse_t, causal=inp.causal,
-                              partials=partials, softmax_scale=inp.qk_scale if inp.qk_scale > 0 else None)
+                              partials=partials, softmax_scale=inp.qk_scale if inp.qk_scale > 0 else None,
+                              causal_pair=causal_pair)
     torch.cuda.synchronize()
     o = out.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
     return o, used, lse_t

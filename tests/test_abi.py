@@ -379,3 +379,26 @@ def test_noalloc_rejects_oversized_split_before_gpu_work():
     po, so = ctypes.c_int(-1), ctypes.c_int(-1)
     rc = lib.raw.fmha_fwd_hd128_mxfp8_auto_noalloc(ctypes.byref(p), None, ctypes.byref(po), ctypes.byref(so), err, 256)
     assert rc == lib.FMHA_ERR_WORKSPACE and b"GV-HOST-WORKSPACE" in err.value, (rc, err.value)
+
+
+
+def test_causal_pair_flag_rules():
+    """FMHA_FLAG_CAUSAL_PAIR (extension): only with the causal flag, only on the 128-row grid (t128 rules; the 256-row
+    vs128 kernel refuses it), and the grid's x extent is then ceil(ceil(S / 128) / 2)."""
+    B, H, S, SK = 2, 4, 1000, 1000
+    a = lib.fill_args(0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 0x6000, 0x7000, B, H, H, S, SK)
+    big = 1 << 40
+    sz = lib.BufferSizes(big, big, big, big, big, big, big, 0, 0)
+    a.flags = lib.FLAG_CAUSAL | lib.FLAG_CAUSAL_PAIR
+    assert lib.validate("t128", a, sz, (4, H, B), HK=H) == (0, "")           # T = 8 -> 4 blocks
+    assert lib.validate("t128", a, sz, (8, H, B), HK=H)[0] == lib.FMHA_ERR_GRID
+    assert lib.validate("vs128", a, sz, (2, H, B), HK=H)[0] == lib.FMHA_ERR_KA_RANGE
+    a.flags = lib.FLAG_CAUSAL_PAIR
+    assert lib.validate("t128", a, sz, (4, H, B), HK=H)[0] == lib.FMHA_ERR_KA_RANGE
+    a.flags = lib.FLAG_CAUSAL | lib.FLAG_CAUSAL_PAIR
+    a.s_seq_len, a.s_Bs, a.s_o_Bs, a.s_descale_q_Bs = 1152, 1152 * H * 128, 1152 * H * 256, 1152 * H * 4   # T = 9
+    assert lib.validate("t128", a, sz, (5, H, B), HK=H) == (0, "")
+    # causal full-sequence shapes run on the 128-row split-tile kernel (where the pairing is), from 4 key tiles on
+    assert lib.uses_split_tiles("vs128", 4, 8, 2048, 2048, causal=True)
+    assert not lib.uses_split_tiles("vs128", 4, 8, 2048, 2048, causal=False)
+    assert not lib.uses_split_tiles("vs128", 4, 8, 2048, 384, causal=True)

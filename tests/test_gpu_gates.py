@@ -68,7 +68,7 @@ def _run_path(gpu, inp, path):
     out, used, _ = gpu_util.run(inp, gpu, path=path, splits=2 if path == "kvsplit" else None)
     if used[0] == "kvsplit":
         return out, (used[1], True), used
-    return out, (0, lib.uses_split_tiles(used[0], B, H, S, SK)), used
+    return out, (0, lib.uses_split_tiles(used[0], B, H, S, SK, inp.causal)), used
 
 
 # A score's MFMA error bound, relative to the sum of its product magnitudes: what the hardware fixture allows

@@ -45,7 +45,7 @@ def _emulated_bar(inp, splits, rows=ROWS, path=None, **kw):
     the emulation handles)."""
     emu = oracle.emulate(inp, splits=splits, rows=rows, **kw)
     ref_stats = oracle.check_fp64(inp, emu, rows=rows)
-    if splits or (path is not None and lib.uses_split_tiles(path, inp.B, inp.H, inp.S, inp.SK)):
+    if splits or (path is not None and lib.uses_split_tiles(path, inp.B, inp.H, inp.S, inp.SK, inp.causal)):
         emu = oracle.emulate(inp, splits=splits, rows=rows, split_tiles=True, **kw)
     return emu, ref_stats
 
@@ -320,7 +320,7 @@ VS128_ST_CASES = [
 def test_parity_vs128_split_tiles(gpu, case):
     name, B, H, HK, S, SK, causal, force = case
     print(f"[case] vs128 split tiles {name}", flush=True)
-    assert lib.uses_split_tiles("vs128", B, H, S, SK)
+    assert lib.uses_split_tiles("vs128", B, H, S, SK, causal)
     inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
     out, used, _ = gpu_util.run(inp, gpu, path=force or "auto")
     assert used[0] == "vs128"
@@ -352,3 +352,40 @@ def test_parity_vs128_split_tiles(gpu, case):
         print(f"[case] vs128 direct launcher {name} vs-single-stream-emulation={dcmp}", flush=True)
         assert dcmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), dcmp
         assert dcmp["max_abs"] <= 0.05, dcmp
+
+
+
+# Extension: the causal q-tile pairing (FMHA_FLAG_CAUSAL_PAIR, the reference's causal_pair, grid.rs:94-111) on the
+# 128-row grid: block x runs query tiles x and T - 1 - x. Each tile is computed exactly as unpaired, so the output must
+# be bit-identical to the unpaired launch; and it meets the causal bar against the emulation on every checked row.
+# (name, B, H, HK, S, SK, path); T odd leaves the middle tile alone; S > SK has rows that see no key; SK < 512 runs
+# the 256-thread t128 kernel (the LUT recipe); B4H8S2048 has more 128-row blocks than CUs, so "auto" pairs it.
+PAIR_CASES = [
+    ("B1H4S1000_SK1337", 1, 4, 4, 1000, 1337, "auto"),
+    ("B1H2S1408_T11", 1, 2, 2, 1408, 1408, "auto"),
+    ("B2H4HK1_S700_gqa4", 2, 4, 1, 700, 700, "auto"),
+    ("S_gt_SK_B1H2S900_SK600", 1, 2, 2, 900, 600, "auto"),
+    ("t128_lut_B1H2S512_SK384", 1, 2, 2, 512, 384, "t128"),
+    ("B4H8S2048_auto_pairs", 4, 8, 8, 2048, 2048, "auto"),
+]
+
+
+@pytest.mark.parametrize("case", PAIR_CASES, ids=[c[0] for c in PAIR_CASES])
+def test_causal_pairing(gpu, case):
+    name, B, H, HK, S, SK, path = case
+    print(f"[case] causal pairing {name}", flush=True)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=True)
+    big = B * H * S * SK > (1 << 24)
+    paired, used, _ = gpu_util.run(inp, gpu, path=path, causal_pair="auto" if big else True)
+    plain, used2, _ = gpu_util.run(inp, gpu, path=path, causal_pair=False)
+    assert used == used2 and (path == "auto" or used[0] == path)
+    assert not np.isnan(oracle.bf16_to_f32(paired)).any()
+    np.testing.assert_array_equal(paired, plain)
+    rows = oracle.first_and_last(S, 128) if big else S
+    emu, ref_stats = _emulated_bar(inp, 0, rows=rows, path=used[0])
+    stats = oracle.check_fp64(inp, paired, rows=rows)
+    cmp = gpu_util.compare_to_emulation(paired, emu, inp, rows)
+    print(f"[case] causal pairing {name} path={used} ours={stats} emulated={ref_stats} vs-emulation={cmp}", flush=True)
+    assert stats["bad"] <= ref_stats["bad"]
+    assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
+    assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
