@@ -29,6 +29,7 @@ KVS_F32_PARTIALS = 0x10000   # include/fmha_mxfp8.h FMHA_KVS_F32_PARTIALS
 KVS_V_SEQ32 = 0x20000        # FMHA_KVS_V_SEQ32
 KVS_SCALE = 0x40000          # FMHA_KVS_SCALE
 FLAG_CAUSAL, FLAG_V_SEQ32, FLAG_SCALE, FLAG_CAUSAL_PAIR = 0x1, 0x2, 0x4, 0x8   # FMHA_FLAG_*
+WORKSPACE_SLOTS = 4          # FMHA_WORKSPACE_SLOTS
 PATH_NAMES = {PATH_VS128: "vs128", PATH_T128: "t128", PATH_KVSPLIT: "kvsplit"}
 PATH_IDS = {v: k for k, v in PATH_NAMES.items()}
 

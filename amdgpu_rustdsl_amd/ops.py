@@ -132,6 +132,11 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     ws, ws_bytes = None, 0
     if want_path == "kvsplit" and not causal:
         ws_bytes = lib.workspace_bytes(B, H, S, want_splits)
+        # room for the entry's workspace slots (consecutive calls then write partials the previous combine did not
+        # just read), unless that would take more than 512 MiB
+        slotted = lib.WORKSPACE_SLOTS * ((ws_bytes + 255) // 256 * 256)
+        if slotted <= 512 << 20:
+            ws_bytes = slotted
         ws = _ws(dev, st, ws_bytes).data_ptr()
     with torch.cuda.device(dev):
         return lib.run_auto(p, ws, ws_bytes, st)

@@ -198,7 +198,9 @@ def main():
     print(f"bench: clock warm-up {clock_steps} steps; {args.steps} steps: events {ms * 1e3:.2f} us/step, wall {ms_wall * 1e3:.2f} "
           f"us/step; reference method: step {ref_ms * 1e3:.2f} us, kernel {kern_name} {kern_ms * 1e3:.2f} us "
           f"(reps step {[round(x * 1e3, 2) for x in step_reps]}, kernel {[round(x * 1e3, 2) for x in kern_reps]})", file=sys.stderr)
-    if kern_ms > ms:
+    # on the single-kernel paths the step is one launch of the same kernel, so the two agree within the clock noise
+    # (about 0.3 %); more than 1 % above both step timings means the kernel leg measured something else
+    if kern_ms > 1.01 * max(ms, ref_ms):
         print(f"bench: WARNING kernel_ms {kern_ms:.5f} > ms_per_step {ms:.5f}", file=sys.stderr)
     traffic = None
     tfile = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")

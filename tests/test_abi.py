@@ -33,6 +33,17 @@ def test_every_declared_symbol_is_exported():
     assert sorted(lib.EXPORTED) == names
 
 
+def test_header_constants_match_the_binding():
+    """The flag bits and sizes the ctypes binding uses are the header's #defines."""
+    src = open(HEADERS[0]).read()
+    defs = {m.group(1): int(m.group(2), 0) for m in re.finditer(r"#define (FMHA_\w+) (0x[0-9a-fA-F]+|\d+)u?", src)}
+    assert defs["FMHA_FLAG_CAUSAL"] == lib.FLAG_CAUSAL and defs["FMHA_FLAG_V_SEQ32"] == lib.FLAG_V_SEQ32
+    assert defs["FMHA_FLAG_SCALE"] == lib.FLAG_SCALE and defs["FMHA_FLAG_CAUSAL_PAIR"] == lib.FLAG_CAUSAL_PAIR
+    assert defs["FMHA_KVS_V_SEQ32"] == lib.KVS_V_SEQ32 and defs["FMHA_KVS_SCALE"] == lib.KVS_SCALE
+    assert defs["FMHA_WORKSPACE_SLOTS"] == lib.WORKSPACE_SLOTS
+    assert defs["FMHA_NOALLOC_SCRATCH_BYTES"] == lib.NOALLOC_SCRATCH_BYTES
+
+
 def test_version_string():
     assert lib.raw.fmha_mxfp8_version().decode().startswith("fmha_mxfp8 gfx950")
 
