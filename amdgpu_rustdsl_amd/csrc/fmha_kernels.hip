@@ -324,6 +324,27 @@ struct Stager {
         const uint32_t dst = w < 2u ? slot_base(lds, kLdsVs, slot, kVsSlot) + 256u * w : lds + kLdsVsSink + 256u * (w - 2u);
         dma4(vs_rsrc((key0 >> 5) + 2u * w, valid && w < 2u), dst, (lane >> 5) * vs_row + 4u * (lane & 31u), 0u);
     }
+    // Copy instruction i (0 .. 2 kN - 1: K chunk i / 2 for even i, V chunk i / 2 for odd i) of dma(), alone, so that a
+    // wave can spread a tile's copies between its MFMAs instead of waiting for the load path in one burst
+    __device__ __forceinline__ void dma_part(int i, uint32_t key0, bool valid, uint32_t slot) const {
+        const bool isv = (i & 1) != 0;
+        const uint8_t* base = isv ? vb : kb;
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(base + (size_t)key0 * k_seq, tile_bytes(key0, valid, k_seq, kD));
+        const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const uint32_t dst = slot_base(lds, isv ? kLdsV : kLdsK, slot, kTileBytes);
+        const uint32_t g = (uint32_t)(i >> 1) * (NT / 64) + w;
+        const uint32_t soff = __builtin_amdgcn_readfirstlane((uint32_t)(i >> 1) * (NT / 8) * k_seq);
+        dma16(r, dst + g * 1024u, dmaoff, soff);
+    }
+    // Direct copy of tile [key0, key0 + 128)'s K-scale words (the words only, no shifted copy: readers use kscale_raw)
+    // into K-scale slot `slot`: waves 0 and 1 copy 64 keys each (lane L: key 64 w + L, its 4 bytes at 4 (64 w + L));
+    // the other waves copy from an empty resource into the sink, so that every wave issues one copy per tile.
+    __device__ __forceinline__ void dma_ks(uint32_t key0, bool valid, uint32_t slot) const {
+        const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63u;
+        const uint32_t dst = w < 2u ? slot_base(lds, kLdsKs, slot, kKsSlot) + 256u * w : lds + kLdsKsDummy + 256u * ((w - 2u) & 3u);
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(ksb + (size_t)key0 * ks_row, tile_bytes(key0, valid && w < 2u, ks_row, 4));
+        dma4(r, dst, (64u * (w & 1u) + lane) * ks_row, 0u);
+    }
     // Register-staged variant (threads 0..127: one word each, block tid / 32, columns 4 (tid % 32) ..)
     __device__ __forceinline__ uint32_t load_vs(uint32_t key0, bool valid) const {
         return __builtin_amdgcn_raw_buffer_load_b32(vs_rsrc(key0 >> 5, valid && tid < 128u), (tid >> 5) * vs_row + 4u * (tid & 31u), 0, 0);
@@ -665,6 +686,11 @@ struct Wave {
     // K-scale word of 32-key block t4 for this lane's key row, read from the copy shifted down by hh bytes so that
     // op_sel byte 2c is the lane half's E8M0 byte 2c + hh
     __device__ __forceinline__ uint32_t kscale(uint32_t ksb, int t4) const { return lds_read4(lane_addr(ksb, kso) + 128u * t4); }
+    // The same from a slot that holds the words only (copied straight from HBM): the upper lane half shifts its word
+    // down one byte itself
+    __device__ __forceinline__ uint32_t kscale_raw(uint32_t ksb, int t4) const {
+        return lds_read4(lane_addr(ksb, 4u * n) + 128u * t4) >> (8u * hh);
+    }
     // E8M0 of PV MFMA (j, dc)'s k-block for this lane: in the scaled MFMA, lane r + 32 kb supplies the scale of row r
     // (column 32 dc + n) over k-block kb, which is 32-key block 2 j + kb of the tile (the S^T tile the P bytes came from)
     __device__ __forceinline__ uint32_t vscale(uint32_t vsb, int j, int dc) const {
@@ -723,7 +749,7 @@ struct Wave {
     // (16 copies of b) is written into s[3] and is the C input of the first MFMA of s[0..2]; s[3] then accumulates
     // in place: no separate seed registers. One K fragment is read one MFMA ahead.
     // (NA accumulators: 32-key blocks KB0 .. KB0 + NA - 1 of the tile)
-    template <int KB0 = 0, int NA>
+    template <int KB0 = 0, int NA, bool RAWKS = false>
     __device__ __forceinline__ void qk_all(uint32_t nslot, v16f (&s)[NA]) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[NA - 1][i] = bias;
@@ -739,7 +765,7 @@ struct Wave {
                 const int g = NA * c + t4;
                 v8i kn = kc;
                 if (g < 2 * NA - 1) kn = kread(g + 1);
-                const uint32_t ksw = kscale(ksb, KB0 + t4);
+                const uint32_t ksw = RAWKS ? kscale_raw(ksb, KB0 + t4) : kscale(ksb, KB0 + t4);
                 s[t4] = qk_mfma(kc, qf, c == 0 ? s[NA - 1] : s[t4], ksw, c);
                 kc = kn;
                 __builtin_amdgcn_sched_barrier(0);
@@ -822,6 +848,78 @@ struct Wave {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[i - NQ - 1][e]);
                 asm volatile("" : "+v"(mx));   // pins this quarter here (the reduction would otherwise sink past the MFMAs)
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (!QK) return 0.0f;
+        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx), __builtin_bit_cast(uint32_t, mx), false, false);
+        return fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]), __builtin_bit_cast(float, (uint32_t)sw[1]));
+    }
+
+    // The MFMA phase of a wave that has its SIMD to itself (the 256-thread block): no second wave converts under its
+    // MFMAs, so it does its own VALU work between them. QK(t+1) (8 MFMAs, into sn, seeded with the bias) runs with the
+    // conversion of S(t) (sc, already rebased) to P(t), one 32-key accumulator after every second MFMA; PV(t) (8 MFMAs
+    // and the 2 row-sum MFMAs) runs with the unmasked row max of S(t+1), as in m_phase_qf. Without QK (the last tile)
+    // the conversion comes first. after_mfma(i) runs behind MFMA i (the caller's tile copies: issued in one burst, they
+    // held the wave ~1,100 cycles per tile at the load path). Operands are read DEPTH MFMAs ahead across the seam,
+    // inside the phase (reading the first ones behind the previous barrier, under the rebase, was slower). Measured
+    // alternatives that were no faster: half of the conversion moved under the PV MFMAs; copies from MFMA 6 on.
+    // Returns the row max.
+    template <bool LUT, bool VS, bool QK, typename F>
+    __device__ __forceinline__ float m_phase_cv(const Recipe& rc, uint32_t vslot, uint32_t kslot, v16f (&sc)[4], v16f (&sn)[4],
+                                                uint32_t (&pw)[4][4], const F& after_mfma) {
+        constexpr int NQ = QK ? 8 : 0, NI = NQ + 8;
+        const uint32_t vb = slot_base(lds, kLdsV, vslot, kTileBytes);
+        const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
+        auto fetch = [&](int i) -> v8i {
+            return i < NQ ? frag(kb, i / 4, 4096u * (uint32_t)(i % 4)) : vfrag(vb, (i - NQ) >> 2, (i - NQ) & 3);
+        };
+        Ring ring;
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) ring[i] = fetch(i);
+        uint32_t ksw[4];
+        v8i qf;
+        if (QK) {
+            const uint32_t ksb = slot_base(lds, kLdsKs, kslot, (uint32_t)kKsSlot);
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) ksw[t4] = kscale_raw(ksb, t4);
+            qf = qfrag(0);
+            sn[3] = splat16(bias);
+        } else {
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, sc[t4], pw[t4]);
+        }
+        uint32_t vsc[8];
+        if (VS) {
+            const uint32_t vsb = slot_base(lds, kLdsVs, vslot, kVsSlot);
+#pragma unroll
+            for (int g = 0; g < 8; ++g) vsc[g] = vscale(vsb, g >> 2, g & 3);
+        }
+        const v8i ones = ones_op();
+        float mx = -1.0e30f;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            if (i + DEPTH < NI) ring[(i + DEPTH) % (DEPTH + 1)] = fetch(i + DEPTH);
+            if (QK && i == 4) qf = qfrag(1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (i < NQ) {
+                const int c = i / 4, t4 = i % 4;
+                sn[t4] = qk_mfma(ring[i % (DEPTH + 1)], qf, c == 0 ? sn[3] : sn[t4], ksw[t4], c);
+            } else {
+                const int j = (i - NQ) >> 2, dc = (i - NQ) & 3;
+                const v8i pf = pfrag(pw, j);
+                if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, pf, lacc, 0, 0, 0, 127, 0, 127);
+                o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ring[i % (DEPTH + 1)], pf, o[dc], 0, 0, 0,
+                                                                         VS ? (int)vsc[i - NQ] : 127, 0, 127);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            after_mfma(i);
+            if (QK && i < NQ && (i & 1) == 0) convert_p<LUT>(rc, sc[i >> 1], pw[i >> 1]);
+            // row max of S(t+1): accumulator a a quarter behind its last QK MFMA (i = 4 + a)
+            if (QK && i >= NQ + 1 && i <= NQ + 4) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sn[i - NQ - 1][e]);
+                asm volatile("" : "+v"(mx));
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -1216,99 +1314,105 @@ __device__ __forceinline__ void attend_pingpong(const Prm& p, uint32_t lds, uint
     else attend_pingpong_group<LUT, SPLIT, false, VS, HV, SC>(p, lds, qtile, head, bidx, split, key_lo, key_hi);
 }
 
-// One 4-wave group (_t128: one wave per SIMD, so each wave overlaps its own VALU with its own MFMAs): S(t) is
-// computed and decided one iteration ahead. Iteration t: [P(t) conversion | QK(t+1)] then [PV(t) | row max of
-// S(t+1)]; the tile t+2 staged through registers lands in slot (t+2) % 3 (tile t-1's: its last read was in
-// iteration t-1), one barrier, then the rebase decision of tile t+1. The last tile runs [P | PV] alone.
-template <bool LUT, bool VS, bool SC, int NT = 256>
-__device__ __forceinline__ void attend_pipelined(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx, uint32_t key_lo,
-                                 uint32_t key_hi) {
+// One 4-wave block of 128 rows with one wave per SIMD (_t128 under its own 256-thread contract). Nothing else runs on
+// the wave's SIMD, so each wave overlaps its own VALU work with its own MFMAs (m_phase_cv): iteration t runs QK(t+1)
+// with the conversion of P(t), then PV(t) with the row max of S(t+1), then (behind the tile's barrier) the rebase
+// decision of S(t+1). S(t) and S(t+1) live in two register sets that swap roles every iteration (the loop body is
+// instantiated twice). Every copy of a tile is direct HBM -> LDS: K and V into a 4-slot ring, the K-scale words
+// (unshifted, kscale_raw) and the V scales into their 4-slot rings. Iteration t issues tile t+3's copies, one behind
+// each of its first MFMAs, into slot (t+3) & 3; it reads K(t+1) and V(t), and the slots it writes, K (t-1) & 3 (last
+// read in iteration t-2) and V (t-1) & 3 (iteration t-1), are free behind barrier t-1. Each barrier waits for the
+// copies of the iteration before: tile t+2 has landed before barrier t, an iteration ahead of its first read.
+template <bool LUT, bool VS, bool SC>
+__device__ __forceinline__ void attend_single_wave(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx) {
+    constexpr int NT = 256;
     const Recipe rc = recipe(LUT);
     Wave<NT> w;
-    w.init(p, lds, qtile, head, bidx, key_hi, wave_id());
+    w.init(p, lds, qtile, head, bidx, p.SK, wave_id());
     const uint32_t kvh = head / p.gqa;
     const bool causal = (p.flags & 1u) != 0;
-    uint32_t key_end = key_hi;
-    if (causal) key_end = (uint32_t)max(0, min((int)key_hi, (int)(qtile * Wave<NT>::ROWS + Wave<NT>::ROWS - 1) + (int)p.SK - (int)p.S + 1));
-    const uint32_t ntiles = key_end > key_lo ? (key_end - key_lo + kTile - 1) / kTile : 0;
+    uint32_t key_end = p.SK;
+    if (causal) key_end = (uint32_t)max(0, min((int)p.SK, (int)(qtile * 128u + 127u) + (int)p.SK - (int)p.S + 1));
+    const uint32_t ntiles = (key_end + kTile - 1) / kTile;
     Stager<NT> st;
     st.init(p.k + (size_t)bidx * p.k_b + kvh * kD, p.v + (size_t)bidx * p.v_b + kvh * kD, p.ks + (size_t)bidx * p.ks_b + kvh * 4u,
             p.k_seq, p.SK, lds);
     if (VS) st.init_vs(p.vs32 + (size_t)bidx * p.vs_b + kvh * kD, p.vs_row);
-    auto key_of = [&](uint32_t t) { return key_lo + t * kTile; };
-
-    v16f s[4];
+    auto key_of = [](uint32_t t) { return t * kTile; };
+    auto slot_of = [](uint32_t t) { return t & 3u; };
+    const uint32_t tblk = (bidx * p.H + head) * ((p.S + 127u) / 128u) + qtile;
+    (void)tblk;
+    FMHA_LDECL;
     if (ntiles > 0) {
-        typename Stager<NT>::Regs r0;
-        st.load_into(r0, key_of(0), true, key_of(0), true);
-        uint32_t vs0 = 0, vs1 = 0;   // V-scale words of tiles 0 and 1 (extension)
-        if (VS) vs0 = st.load_vs(key_of(0), true);
-        st.load(key_of(1), ntiles > 1, key_of(1), ntiles > 1);
-        if (VS) vs1 = st.load_vs(key_of(1), ntiles > 1);
+        st.init_dma();
+        // every copy of a tile: K, V, the K-scale words and (extension) the V scales; all three prologue tiles at once
+        auto copy_tile = [&](uint32_t u) {
+            st.dma(key_of(u), u < ntiles, slot_of(u), key_of(u), u < ntiles, slot_of(u));
+            st.dma_ks(key_of(u), u < ntiles, slot_of(u));
+            if (VS) st.dma_vs(key_of(u), u < ntiles, slot_of(u));
+        };
+        copy_tile(0);
+        copy_tile(1);
+        copy_tile(2);
         w.commit_q();
-        st.store_from(r0, 0, 0);
-        if (ntiles > 1) st.store(1, 1);
-        if (VS) {
-            st.store_vs(vs0, 0);
-            st.store_vs(vs1, 1);
-        }
-        block_barrier();
-        if (w.active(key_of(0))) {
-            w.qk_all(0, s);
-            float m0 = 0.0f;
-            if (SC) w.scale_s(s, m0);
-            if (w.needs_mask(key_of(0))) w.apply_mask(s, key_of(0));
-            rebase<LUT>(rc, row_max(s), s, w.o, w.lacc, w.bias, w.bw, w.qrm);
-        }
-        uint32_t slot = 0;
-        for (uint32_t t = 0; t + 1 < ntiles; ++t) {
-            const uint32_t nslot = slot == 2u ? 0u : slot + 1u;
-            const uint32_t sslot = nslot == 2u ? 0u : nslot + 1u;   // slot of tile t+2
-            st.load(key_of(t + 2), t + 2 < ntiles, key_of(t + 2), t + 2 < ntiles);
-            uint32_t vs2 = 0;
-            if (VS) vs2 = st.load_vs(key_of(t + 2), t + 2 < ntiles);
-            const bool act = w.active(key_of(t)), act_next = w.active(key_of(t + 1));
-            uint32_t pw[4][4];
-            if (act_next) {
-                // P(t) conversion interleaved with k-half 0 of QK(t+1) (accumulator t4 of S(t) is dead once
-                // converted; a separate seed, this path has the registers), then k-half 1
-                const uint32_t kb = slot_base(w.lds, kLdsK, nslot, kTileBytes), ksb = slot_base(w.lds, kLdsKs, nslot, (uint32_t)kKsSlot);
-                v16f seed;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) seed[i] = w.bias;
-                const v8i q0 = w.qfrag(0);
-#pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) {
-                    convert_p<LUT>(rc, s[t4], pw[t4]);
-                    s[t4] = w.qk_mfma(w.frag(kb, 0, 4096u * t4), q0, seed, w.kscale(ksb, t4), 0);
-                }
-                const v8i q1 = w.qfrag(1);
-#pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) s[t4] = w.qk_mfma(w.frag(kb, 1, 4096u * t4), q1, s[t4], w.kscale(ksb, t4), 1);
-            } else if (act) {
-#pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
+        // VMEM operations per tile: the K and V copies, the K-scale copy and (extension) the V-scale copy
+        constexpr int kOps = 2 * Stager<NT>::kN + 1 + (VS ? 1 : 0);
+        block_barrier_keep_dma<0, kOps>();   // tiles 0 and 1 have landed; tile 2's copies stay in flight
+        v16f sa[4], sb[4];
+        {
+            w.template qk_all<0, 4, true>(0, sa);
+            float m0 = row_max(sa);
+            if (SC) w.scale_s(sa, m0);
+            if (w.needs_mask(key_of(0))) {
+                w.apply_mask(sa, key_of(0));
+                m0 = row_max(sa);
             }
-            if (act) w.template pv_all<VS>(slot, pw);
-            float m = 0.0f;
-            if (act_next) {
-                if (SC) w.scale_s(s, m);
-                if (w.needs_mask(key_of(t + 1))) w.apply_mask(s, key_of(t + 1));
-                m = row_max(s);
-            }
-            if (t + 2 < ntiles) st.store(sslot, sslot);
-            if (VS && t + 2 < ntiles) st.store_vs(vs2, sslot);
-            block_barrier();
-            if (act_next) rebase<LUT>(rc, m, s, w.o, w.lacc, w.bias, w.bw, w.qrm);
-            slot = nslot;
+            rebase<LUT>(rc, m0, sa, w.o, w.lacc, w.bias, w.bw, w.qrm);
         }
-        if (w.active(key_of(ntiles - 1))) {
+        uint32_t t = 0;
+        // iteration t: S(t) in sc (rebased), S(t+1) into sn
+        auto step = [&](v16f (&sc)[4], v16f (&sn)[4]) {
+            FMHA_LMARK(p, tblk, t, 0);
             uint32_t pw[4][4];
+            // the copies of tile t+3, one instruction behind each of the phase's first MFMAs
+            const uint32_t u = t + 3;
+            auto copies = [&](int i) {
+                if (i < 2 * Stager<NT>::kN) st.dma_part(i, key_of(u), u < ntiles, slot_of(u));
+                else if (i == 2 * Stager<NT>::kN) st.dma_ks(key_of(u), u < ntiles, slot_of(u));
+                else if (VS && i == 2 * Stager<NT>::kN + 1) st.dma_vs(key_of(u), u < ntiles, slot_of(u));
+            };
+            float m = w.template m_phase_cv<LUT, VS, true>(rc, slot_of(t), slot_of(t + 1), sc, sn, pw, copies);
+            if (SC) w.scale_s(sn, m);
+            if (w.needs_mask(key_of(t + 1))) {
+                w.apply_mask(sn, key_of(t + 1));
+                m = row_max(sn);
+            }
+            FMHA_LMARK(p, tblk, t, 1);
+            block_barrier_keep_dma<0, kOps>();   // tile t+2 has landed (this iteration's operations stay in flight)
+            FMHA_LMARK(p, tblk, t, 2);
+            rebase<LUT>(rc, m, sn, w.o, w.lacc, w.bias, w.bw, w.qrm);
+            FMHA_LMARK(p, tblk, t, 3);
+            ++t;
+        };
+        auto last = [&](v16f (&sc)[4]) {
+            uint32_t pw[4][4];
+            (void)w.template m_phase_cv<LUT, VS, false>(rc, slot_of(t), slot_of(t), sc, sc, pw, [](int) {});
+        };
+        // two iterations per trip, so the sets swap without copies (one copy when the last tile's S is in sb: with a
+        // second instantiation of the last tile the register allocation spilled)
+        while (t + 1 < ntiles) {
+            step(sa, sb);
+            if (t + 1 >= ntiles) {
 #pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
-            w.template pv_all<VS>(slot, pw);
+                for (int a = 0; a < 4; ++a) sa[a] = sb[a];
+                break;
+            }
+            step(sb, sa);
         }
+        last(sa);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no copy into LDS outlives the loop
     }
+    FMHA_LFLUSH(p, tblk);
     epilogue<false>(p, w, head, bidx, 0, rc, true);
 }
 
@@ -1366,11 +1470,11 @@ __device__ __forceinline__ void full_kernel(uint32_t lds) {
             const uint32_t qt = pass == 0u ? x : nt - 1u - x;
             if (pass > 0u) block_barrier();
             if (p.vs32) {
-                if (lut) attend_pipelined<true, true, SC>(p, lds, qt, head, z, 0, p.SK);
-                else attend_pipelined<false, true, SC>(p, lds, qt, head, z, 0, p.SK);
+                if (lut) attend_single_wave<true, true, SC>(p, lds, qt, head, z);
+                else attend_single_wave<false, true, SC>(p, lds, qt, head, z);
             } else {
-                if (lut) attend_pipelined<true, false, SC>(p, lds, qt, head, z, 0, p.SK);
-                else attend_pipelined<false, false, SC>(p, lds, qt, head, z, 0, p.SK);
+                if (lut) attend_single_wave<true, false, SC>(p, lds, qt, head, z);
+                else attend_single_wave<false, false, SC>(p, lds, qt, head, z);
             }
         }
     }
