@@ -111,6 +111,14 @@ bool vs128_split_tiles(int64_t B, int64_t H, int64_t S, int64_t SK, bool causal)
     return (causal || (S + 255) / 256 * H * B <= 128) && t128_split_tiles(SK);
 }
 
+// With the LUT recipe (fewer than 4 key tiles) such a half-chip vs128 grid runs on the 256-thread t128 kernel instead:
+// the same order and bits as the vs128 kernel (both take every tile whole), on twice the blocks. Measured at B4H8S1024
+// SK256, B2H8S2048 SK384 and B1H8S4096 SK128: 10.4 / 12.6 / 7.7 us against 11.9 / 14.3 / 9.5 (above 128 blocks of
+// 256 rows the vs128 kernel stays ahead: B8H8S2048 SK256 25.4 against 36.4 us).
+bool vs128_on_t128(int64_t B, int64_t H, int64_t S, int64_t SK) {
+    return (S + 255) / 256 * H * B <= 128 && !t128_split_tiles(SK);
+}
+
 fmha_internal::ModuleCache<9> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
 
 int get_functions(hipFunction_t** out, char* err, size_t errlen) { return g_fmha.get(out, err, errlen); }
@@ -433,6 +441,9 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
             kern = t128_kernel((uint32_t)SK, scaled, &block);
         } else if (vs128_split_tiles(B, H, S, SK, p->causal != 0)) {
             kern = scaled ? K_T128ST_SC : K_T128ST;   // same kernarg layout, 128-row grid
+            kgx = (uint32_t)((S + 127) / 128);
+        } else if (vs128_on_t128(B, H, S, SK)) {
+            kern = t128_kernel((uint32_t)SK, scaled, &block);   // the 256-thread kernel: same kernargs, 128-row grid
             kgx = (uint32_t)((S + 127) / 128);
         } else {
             kern = scaled ? K_VS128_SC : K_VS128;
