@@ -1,6 +1,6 @@
 """Benchmark of the MXFP8 FMHA forward (hd128) on one MI355X: the reference's headline metric.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg5|cfg1] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg5|cfg1|quant|t128] [--no-cpu]
 
 One step = one call of fmha_fwd_hd128_mxfp8_auto (dispatch + validate + launch, plus the combine on the KV-split
 path) on inputs already resident in HBM. Prints ONE JSON line. TFLOP/s = 4 B H S SK 128 / t (algorithmic,
@@ -43,7 +43,13 @@ WORKLOADS = {
     "cfg1": (1, 1, 1, 256, 256, False, "auto", None, "B1H1S256 (configs[0], t128)"),
     # the on-GPU quantisers producing cfg2's inputs from bf16 (not the headline metric; an HBM-bound side path)
     "quant": (4, 8, 8, 2048, 2048, False, None, None, "MXFP8 quantisation of B4H8S2048 bf16 Q, K, V"),
+    # the reference-named _t128 kernel under its own contract (256 threads, grid (ceil(S/128), H, B)) on every shape the
+    # reference publishes for the t128 path; not the headline metric
+    "t128": (None, 8, 8, None, None, False, "t128", None, "fmha_fwd_hd128_mxfp8_v3_t128, 256 threads, the 8 published t128 shapes"),
 }
+# docs/perf-matrix.md: (B, S, SK) -> the reference's TF/s on the t128 path
+T128_PUBLISHED = [((1, 512, 512), 104.8), ((1, 1024, 1024), 283.8), ((2, 512, 512), 204.8), ((2, 1024, 1024), 538.5),
+                  ((4, 512, 512), 390.2), ((1, 1000, 1000), 256.7), ((1, 2048, 1337), 554.1), ((1, 1000, 1337), 283.4)]
 
 
 def flops_of(B, H, S, SK, causal):
@@ -119,6 +125,8 @@ def main():
 
     if args.workload == "quant":
         return main_quant(args, torch, lib, ops)
+    if args.workload == "t128":
+        return main_t128(args, torch, lib, ops)
     B, H, HK, S, SK, causal, path, splits, desc = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -237,6 +245,71 @@ def main():
         line["cpu_baseline"] = cpu_baseline(B, H, HK, S, SK, causal)
     else:
         line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+def main_t128(args, torch, lib, ops):
+    """The reference-named fmha_fwd_hd128_mxfp8_v3_t128 launched as a reference launcher would (fmha_mxfp8_launch_t128:
+    block 256, grid (ceil(S/128), H, B)) on each published t128 shape, timed by the reference's method (100 launches,
+    median of 5), after the clock warm-up. value = the smallest ratio to the reference's published TF/s; the per-shape
+    figures are in config.shapes."""
+    import ctypes
+    _, H, HK, _, _, _, _, _, desc = WORKLOADS["t128"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    st = stream.cuda_stream
+    shapes, keep = [], []
+    for (B, S, SK), ref in T128_PUBLISHED:
+        q, k, v, qs, ks, vs = ops.random_inputs(B, H, S, SK, HK=HK, device=dev, seed=1234)
+        out = torch.empty(B, S, H, 128, dtype=torch.bfloat16, device=dev)
+        a = lib.fill_args(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), qs.data_ptr(), ks.data_ptr(), vs.data_ptr(),
+                          B, H, HK, S, SK)
+        grid = (math.ceil(S / 128), H, B)
+        sz = lib.BufferSizes(ops._cap(q), ops._cap(k), ops._cap(v), ops._cap(out), ops._cap(qs), ops._cap(ks), ops._cap(vs), 0, 0)
+        rc, msg = lib.validate("t128", a, sz, grid, HK=HK)
+        assert rc == 0, msg
+        keep.append((q, k, v, qs, ks, vs, out, a))
+        shapes.append(((B, S, SK), ref, a, grid))
+    rcs = []
+    def launcher(a, grid):
+        return lambda: rcs.append(lib.raw.fmha_mxfp8_launch_t128(ctypes.byref(a), *grid, st))
+    # clock warm-up on the first shape
+    f0 = launcher(shapes[0][2], shapes[0][3])
+    t_end = time.perf_counter() + CLOCK_WARMUP_MS / 1e3
+    while time.perf_counter() < t_end:
+        for _ in range(50):
+            f0()
+        torch.cuda.synchronize()
+    res = []
+    for (B, S, SK), ref, a, grid in shapes:
+        f = launcher(a, grid)
+        for _ in range(max(args.warmup, 20)):
+            f()
+        reps = []
+        for _ in range(REF_REPS):
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(REF_LAUNCHES):
+                f()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            reps.append(e0.elapsed_time(e1) / REF_LAUNCHES)
+        ms = sorted(reps)[len(reps) // 2]
+        tf = flops_of(B, H, S, SK, False) / (ms * 1e-3) / 1e12
+        res.append({"B": B, "S": S, "SK": SK, "us": round(ms * 1e3, 2), "tflops": round(tf, 1), "reference": ref,
+                    "ratio": round(tf / ref, 3)})
+        print(f"bench t128: B{B}H{H}S{S}SK{SK} {ms * 1e3:.2f} us {tf:.1f} TF/s ({tf / ref:.3f}x the reference)", file=sys.stderr)
+    assert all(rc == 0 for rc in rcs), f"kernel launches failed: {sorted(set(rcs))}"
+    worst = min(r["ratio"] for r in res)
+    line = {
+        "metric": "fmha_fwd_hd128_mxfp8_v3_t128 under its 256-thread contract / the reference's published t128 TF/s (worst shape)",
+        "value": worst, "unit": "ratio", "n_gpus": 1, "steps": REF_LAUNCHES * REF_REPS, "warmup": max(args.warmup, 20),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": worst, "dtype": "e4m3 (MXFP8, E8M0/32 scales, fp32 accumulate)",
+        "data": "synthetic: N(0,1) Q/K/V quantised to MXFP8 like the reference's REF_DATA=normal generator, drawn on the GPU",
+        "config": {"workload": desc, "H": H, "shapes": res},
+    }
     print(json.dumps(line), flush=True)
 
 
