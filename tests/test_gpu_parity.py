@@ -101,6 +101,7 @@ def test_parity_causal(gpu, case):
     assert stats["bad"] <= ref_stats["bad"]
     assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
     assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
+    assert cmp["max_abs"] <= 0.25, cmp   # causal: looser than the 0.05 of the unmasked cases (observed up to 0.094)
     if S > SK:
         o = oracle.bf16_to_f32(out).reshape(B, S, H, 128)
         assert (o[:, : S - SK] == 0).all()   # query i sees keys t <= i + SK - S: none for i < S - SK
@@ -335,8 +336,9 @@ def test_parity_vs128_split_tiles(gpu, case):
     assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
     # no element-wise maximum under the causal mask, as in test_parity_causal: in the first rows a few keys carry the
     # whole weight, so one fp8 rounding of P that the MFMA's inexact sum moves shifts an output by a few % of |V|
+    # under the causal mask a looser element-wise bound (observed up to 0.094 over the causal cases)
+    assert cmp["max_abs"] <= (0.25 if causal else 0.05), cmp
     if not causal:
-        assert cmp["max_abs"] <= 0.05, cmp
         # the direct vs128 launcher keeps the 256-row kernel its grid names (the single-stream order), correct here too
         import ctypes, math, torch
         q, k, v, qs, ks, vs = gpu_util.upload(inp, gpu)
@@ -389,3 +391,4 @@ def test_causal_pairing(gpu, case):
     assert stats["bad"] <= ref_stats["bad"]
     assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
     assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
+    assert cmp["max_abs"] <= 0.25, cmp
