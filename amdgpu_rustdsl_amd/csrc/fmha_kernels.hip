@@ -280,26 +280,19 @@ __device__ inline void dma4(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint
                  : "memory");
 }
 
-// Register-staged copy of one 128-key tile (K and V: 16 KiB each; K scales: 512 B) from HBM into an LDS ring
-// slot: load() issues the buffer loads into VGPRs, store() writes them (after the slot is free) with ds_write_b128.
-// Thread tid moves 16-byte chunk (tid & 7) of rows i NT/8 + tid/8, i < kN: each 8-thread group reads one
-// contiguous 128-byte row. The chunk lands at (chunk ^ swz(row)); NT/8 is a multiple of 16, so the swizzle and
-// the per-thread offsets are the same for every i.
-// The tile's first key rides in the buffer resource's base and the resource's size ends at the sequence's last key,
-// so rows past the end (the last, partial tile) read zeros from the range check, and a tile index past the range
-// gets an empty resource (no memory traffic): one branch-free code path, so the compiler keeps a single register set
-// for the staged tile (merging several sets cost a copy behind a wait for every load, which serialised the prefetch).
-// (Staging through VGPRs instead of buffer_load ... lds keeps every LDS read free of the compiler's conservative
-// vmcnt(0) before reads that might alias an in-flight LDS DMA.)
+// The copies of one 128-key tile (K and V: 16 KiB each; K scales: 512 B; per-32-key V scales: 512 B) from HBM into
+// its LDS ring slots. K and V go by direct copies (buffer_load ... lds, dma below); the 512-thread kernels stage the
+// K-scale words through a register (the upper k-group's copy shifted down one byte), the 256-thread kernel copies the
+// words directly (dma_ks) and shifts on read. The tile's first key rides in the buffer resource's base and the
+// resource's size ends at the sequence's last key, so rows past the end (the last, partial tile) read zeros from the
+// range check, and a tile index past the range gets an empty resource (no memory traffic): one branch-free code path.
 template <int NT>
 struct Stager {
     static constexpr int kN = kTileBytes / (NT * 16);   // 16-byte chunks per thread per 16 KiB tile
     const uint8_t *kb, *vb, *ksb;
-    uint32_t voff[kN];  // (i NT/8 + tid/8) k_seq + 16 (tid & 7)
     uint32_t ksoff;     // K-scale load offset: key (tid & 127) for tid < 256, out of range (zeros) beyond
-    uint32_t kswoff;    // K-scale LDS write offset in a slot (tid < 256: word tid; beyond: the sink), see store_from
+    uint32_t kswoff;    // K-scale LDS write offset in a slot (tid < 256: word tid; beyond: the sink)
     uint32_t ksshift;   // 0 for the words (tid < 128), 8 for the shifted copies (128 <= tid < 256)
-    uint32_t woff;      // (tid / 8) 128 + 16 ((tid & 7) ^ swz(tid / 8))
     uint32_t tid, k_seq, ks_row, SK, lds;
     const uint8_t* vsb; // per-32-key V scales of this (batch, KV head) (extension; unused otherwise)
     uint32_t vs_row;    // bytes between consecutive 32-key blocks of the V-scale tensor (HK 128)
@@ -345,13 +338,6 @@ struct Stager {
         const __amdgpu_buffer_rsrc_t r = make_rsrc(ksb + (size_t)key0 * ks_row, tile_bytes(key0, valid && w < 2u, ks_row, 4));
         dma4(r, dst, (64u * (w & 1u) + lane) * ks_row, 0u);
     }
-    // Register-staged variant (threads 0..127: one word each, block tid / 32, columns 4 (tid % 32) ..)
-    __device__ __forceinline__ uint32_t load_vs(uint32_t key0, bool valid) const {
-        return __builtin_amdgcn_raw_buffer_load_b32(vs_rsrc(key0 >> 5, valid && tid < 128u), (tid >> 5) * vs_row + 4u * (tid & 31u), 0, 0);
-    }
-    __device__ __forceinline__ void store_vs(uint32_t word, uint32_t slot) const {
-        if (tid < 128u) lds_write4(slot_base(lds, kLdsVs, slot, kVsSlot) + 4u * tid, word);
-    }
 
     __device__ void init(const uint8_t* kb_, const uint8_t* vb_, const uint8_t* ksb_, uint32_t k_seq_, uint32_t SK_, uint32_t lds_) {
         // wave-uniform base pointers (readfirstlane states it), so the per-tile resource arithmetic stays scalar
@@ -361,30 +347,12 @@ struct Stager {
         ks_row = k_seq_ >> 5;
         SK = SK_;
         lds = lds_;
-        const uint32_t row = tid >> 3, c = tid & 7u;
-#pragma unroll
-        for (int i = 0; i < kN; ++i) voff[i] = (row + (uint32_t)(i * NT / 8)) * k_seq + (c << 4);
         ksoff = tid < 256u ? (tid & 127u) * ks_row : 0x80000000u;
         kswoff = tid < 256u ? tid * 4u : 0u;
         ksshift = tid < 128u ? 0u : 8u;
-        woff = row * 128u + ((c ^ swz(row)) << 4);
     }
 
-    // Loads tile [key0, key0 + 128) when `valid` (zeros past SK), nothing when not. The resource sizes are wave-uniform
-    // scalar arithmetic: rem = SK - 1 - key0 keys follow the tile's first, so the valid bytes are rem k_seq + 128.
-    struct Regs {
-        v4i kr[kN], vr[kN];
-        uint32_t ksr;
-    };
-
-    Regs cur;   // the tile staged between its load (MFMA phase) and its store (next VALU phase)
-
-    // Loads this thread's share of K tile [kkey0, kkey0 + 128) (with its scales) and of V tile [vkey0, vkey0 + 128);
-    // a part that is not valid reads zeros and no memory.
-    __device__ __forceinline__ void load(uint32_t kkey0, bool kvalid, uint32_t vkey0, bool vvalid) {
-        load_into(cur, kkey0, kvalid, vkey0, vvalid);
-    }
-    __device__ __forceinline__ void store(uint32_t kslot, uint32_t vslot) const { store_from(cur, kslot, vslot); }
+    uint32_t ksr;   // the K-scale word of the next tile, loaded in one VALU phase and stored in the next
 
     // resource size of a tile starting at key0: rem = SK - 1 - key0 keys follow the first, rem stride + tail bytes
     __device__ __forceinline__ uint32_t tile_bytes(uint32_t key0, bool valid, uint32_t stride, int tail) const {
@@ -392,23 +360,11 @@ struct Stager {
         return valid ? (uint32_t)max(rem * (int)stride + tail, 0) : 0u;
     }
 
-    __device__ __forceinline__ void load_into(Regs& r, uint32_t kkey0, bool kvalid, uint32_t vkey0, bool vvalid) const {
-        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb + (size_t)kkey0 * k_seq, tile_bytes(kkey0, kvalid, k_seq, kD));
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb + (size_t)vkey0 * k_seq, tile_bytes(vkey0, vvalid, k_seq, kD));
-        const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksb + (size_t)kkey0 * ks_row, tile_bytes(kkey0, kvalid, ks_row, 4));
-#pragma unroll
-        for (int i = 0; i < kN; ++i) {
-            r.kr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rk, voff[i], 0, 0));
-            r.vr[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, voff[i], 0, 0));
-        }
-        r.ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, ksoff, 0, 0);
-    }
-
     // Direct HBM -> LDS copies (buffer_load_dwordx4 ... lds), no VGPR round trip: copy i of wave w writes LDS rows
     // [8 g, 8 g + 8) of the slot, g = i NT/64 + w, lane L the 16 bytes at (8 g + L / 8) 128 + 16 (L & 7), which hold logical
     // chunk (L & 7) ^ swz(row) of that row. Row steps of NT/8 (a multiple of 16) leave swz unchanged, so the lane's
     // source offset is the same for every copy (dmaoff) plus a scalar (i NT/8) rows. A lane past the resource's end
-    // gets zeros, exactly as the register-staged path.
+    // gets zeros.
     uint32_t dmaoff;
     __device__ __forceinline__ void init_dma() {
         const uint32_t row = 8u * (tid >> 6) + ((tid & 63u) >> 3);
@@ -430,9 +386,9 @@ struct Stager {
     // The K-scale words of tile [kkey0, kkey0 + 128) into ksr (register-staged: the upper k-group's copy is shifted)
     __device__ __forceinline__ void load_ks(uint32_t kkey0, bool kvalid) {
         const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksb + (size_t)kkey0 * ks_row, tile_bytes(kkey0, kvalid, ks_row, 4));
-        cur.ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, ksoff, 0, 0);
+        ksr = __builtin_amdgcn_raw_buffer_load_b32(rks, ksoff, 0, 0);
     }
-    __device__ __forceinline__ void store_ks(uint32_t kslot) const { store_ks_word(cur.ksr, kslot); }
+    __device__ __forceinline__ void store_ks(uint32_t kslot) const { store_ks_word(ksr, kslot); }
     // the same through a register the caller holds (the prologue loads several tiles' words at once)
     __device__ __forceinline__ uint32_t ks_word(uint32_t kkey0, bool kvalid) const {
         const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksb + (size_t)kkey0 * ks_row, tile_bytes(kkey0, kvalid, ks_row, 4));
@@ -443,19 +399,6 @@ struct Stager {
         lds_write4(ksw_base + kswoff, word >> ksshift);
     }
 
-    __device__ __forceinline__ void store_from(const Regs& r, uint32_t kslot, uint32_t vslot) const {
-        const uint32_t kb_ = slot_base(lds, kLdsK, kslot, kTileBytes) + woff, vb_ = slot_base(lds, kLdsV, vslot, kTileBytes) + woff;
-#pragma unroll
-        for (int i = 0; i < kN; ++i) {
-            lds_write16(kb_ + i * NT * 16, r.kr[i]);
-            lds_write16(vb_ + i * NT * 16, r.vr[i]);
-        }
-        // threads 0..127: the scale word of key tid; 128..255: the word of key tid - 128 shifted down one byte (read by
-        // the lanes of the upper k-group); the rest write the sink. Unconditional, so the load is not sunk into a
-        // branch (and issued late) by the compiler.
-        const uint32_t ksw_base = tid < 256u ? slot_base(lds, kLdsKs, kslot, kKsSlot) : lds + kLdsKsDummy;
-        lds_write4(ksw_base + kswoff, r.ksr >> ksshift);
-    }
 };
 
 // Workgroup barrier that is also a compiler memory barrier (no LDS access moves across it): drains this wave's
@@ -718,31 +661,6 @@ struct Wave {
         // scaled fp8 MFMA: A = K (rows = keys), B = Q^T (columns = queries), E8M0 scales per 32 of k
         return c == 0 ? __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf, qf, c_in, 0, 0, 0, (int)ksw, 0, sq[0])
                       : __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(kf, qf, c_in, 0, 0, 2, (int)ksw, 0, sq[1]);
-    }
-
-    // PV of one tile: O^T += V^T P^T (8 MFMAs) and the row sums of P (2 MFMAs). Each V^T fragment is read one MFMA
-    // ahead; a scheduling fence after every MFMA keeps the compiler from hoisting the phase's 32 reads to its top.
-    template <bool VS = false>
-    __device__ __forceinline__ void pv_all(uint32_t slot, const uint32_t (&pw)[4][4]) {
-        const uint32_t vb = slot_base(lds, kLdsV, slot, kTileBytes);
-        uint32_t vsc[8];
-        if (VS) {
-            const uint32_t vsb = slot_base(lds, kLdsVs, slot, kVsSlot);
-#pragma unroll
-            for (int g = 0; g < 8; ++g) vsc[g] = vscale(vsb, g >> 2, g & 3);
-        }
-        v8i vf = vfrag(vb, 0, 0);
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            const int j = g >> 2, dc = g & 3;
-            const v8i pf = pfrag(pw, j);
-            v8i vn = vf;
-            if (g < 7) vn = vfrag(vb, (g + 1) >> 2, (g + 1) & 3);
-            if (dc == 0) lacc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones_op(), pf, lacc, 0, 0, 0, 127, 0, 127);
-            o[dc] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, o[dc], 0, 0, 0, VS ? (int)vsc[g] : 127, 0, 127);
-            vf = vn;
-            __builtin_amdgcn_sched_barrier(0);
-        }
     }
 
     // S(t+1): k-half 0 of all four 32-key accumulators, then k-half 1 (one Q fragment live at a time). The seed
