@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import oracle
-from amdgpu_rustdsl_amd import lib
+from amdgpu_rustdsl_amd import lib, ops
 from tests import gpu_util
 
 pytestmark = pytest.mark.gpu
@@ -392,3 +392,40 @@ def test_causal_pairing(gpu, case):
     assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
     assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
     assert cmp["max_abs"] <= 0.25, cmp
+
+
+# Extension: KV-split workspace slots. A workspace of k times the reference's size is used as min(k, 4) slots taken in
+# turn by consecutive calls; each slot holds a whole call's partials, so every call must give the bits of the
+# one-slot call. The workspace is filled with NaN bytes first: a call reading another slot's (or no) partials would
+# show as NaN or as a difference.
+def test_workspace_slots(gpu):
+    import torch
+    inp = oracle.Inputs(1, 8, 512, 4096, seed_mix=11)
+    print("[case] workspace slots B1H8S512_SK4096", flush=True)
+    q, k, v, qs, ks, vs = gpu_util.upload(inp, gpu)
+    B, H, S, SK = inp.B, inp.H, inp.S, inp.SK
+    used = lib.select_path(B, H, S, SK)
+    assert used[0] == "kvsplit"
+    need = lib.workspace_bytes(B, H, S, used[1])
+    st = torch.cuda.current_stream(gpu).cuda_stream
+
+    def call(ws, nbytes):
+        out = torch.full((B, S, H, 128), float("nan"), dtype=torch.bfloat16, device=gpu)
+        p = lib.Params()
+        p.o, p.q, p.k, p.v = out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr()
+        p.q_descale, p.k_descale, p.v_descale, p.lse = qs.data_ptr(), ks.data_ptr(), vs.data_ptr(), None
+        p.bytes_q, p.bytes_k, p.bytes_v, p.bytes_o = ops._cap(q), ops._cap(k), ops._cap(v), ops._cap(out)
+        p.bytes_q_descale, p.bytes_k_descale, p.bytes_v_descale = ops._cap(qs), ops._cap(ks), ops._cap(vs)
+        p.B, p.H, p.HK, p.S, p.SK = B, H, inp.HK, S, SK
+        p.path, p.splits = -1, 0
+        assert lib.run_auto(p, ws.data_ptr(), nbytes, st) == used
+        torch.cuda.synchronize()
+        return out.view(torch.int16).cpu().numpy()
+
+    one = torch.full((need,), 0xFF, dtype=torch.uint8, device=gpu)
+    want = call(one, need)
+    assert not np.isnan(oracle.bf16_to_f32(want.view(np.uint16))).any()
+    stride = (need + 255) // 256 * 256
+    four = torch.full((lib.WORKSPACE_SLOTS * stride,), 0xFF, dtype=torch.uint8, device=gpu)
+    for i in range(2 * lib.WORKSPACE_SLOTS + 1):
+        np.testing.assert_array_equal(call(four, four.numel()), want, err_msg=f"call {i}")
