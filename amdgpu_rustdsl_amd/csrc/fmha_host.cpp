@@ -78,7 +78,7 @@ namespace {
 using fmha_internal::fail;
 using fmha_internal::set_err;
 
-const char* const kKernelNames[9] = {
+const char* const kKernelNames[10] = {
     "fmha_fwd_hd128_mxfp8_v3_vs128",
     "fmha_fwd_hd128_mxfp8_v3_t128",
     "fmha_fwd_hd128_mxfp8_v3_kvsplit",
@@ -90,9 +90,11 @@ const char* const kKernelNames[9] = {
     // extension kernels: t128's grid with 512 threads, the two wave groups splitting each tile's keys
     "fmha_fwd_hd128_mxfp8_v3_t128_split_tiles",
     "fmha_fwd_hd128_mxfp8_v3_t128_split_tiles_scaled",
+    // extension kernel: the combine with the splits spread over 4 waves (more than 8 partials per row)
+    "fmha_fwd_hd128_mxfp8_v3_kvsplit_combine_wide",
 };
 enum { K_VS128 = 0, K_T128 = 1, K_KVSPLIT = 2, K_COMBINE = 3, K_VS128_SC = 4, K_T128_SC = 5, K_KVSPLIT_SC = 6, K_T128ST = 7,
-       K_T128ST_SC = 8 };
+       K_T128ST_SC = 8, K_COMBINE_WIDE = 9 };
 
 // t128's shapes run on the split-tile kernel (512 threads) unless the whole sequence has fewer than 4 key tiles (the
 // LUT recipe, state.rs:75-77), which keeps the reference's order on the one-wave-per-SIMD kernel (256 threads)
@@ -119,7 +121,7 @@ bool vs128_on_t128(int64_t B, int64_t H, int64_t S, int64_t SK) {
     return (S + 255) / 256 * H * B <= 128 && !t128_split_tiles(SK);
 }
 
-fmha_internal::ModuleCache<9> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
+fmha_internal::ModuleCache<10> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
 
 int get_functions(hipFunction_t** out, char* err, size_t errlen) { return g_fmha.get(out, err, errlen); }
 
@@ -236,9 +238,26 @@ bool empty_split(i64 SK, i64 splits) {
     return !((splits - 1) * tps < ntiles);
 }
 
+// KV-split fill (extension): the reference's `splits` chunks, each divided into `sub` consecutive key ranges, so that
+// a grid of few blocks fills the CUs. sub doubles (up to 8) while the grid stays within the CU count and every range
+// keeps at least 4 key tiles (the recipe of the reference's splits, which have at least 4). The combine merges the
+// splits x sub partials.
+i64 kv_fill(i64 B, i64 H, i64 S, i64 SK, i64 splits) {
+    const i64 blocks = (S + 255) / 256 * H * B * splits, tiles = (SK + 127) / 128;
+    i64 sub = 1;
+    while (sub < 8 && blocks * sub * 2 <= (i64)cu_count() && tiles >= 4 * splits * sub * 2 && !empty_split(SK, splits * sub * 2))
+        sub *= 2;
+    return sub;
+}
+
 }  // namespace
 
 extern "C" {
+
+int fmha_mxfp8_kv_partials(int64_t B, int64_t H, int64_t S, int64_t SK, int splits) {
+    if (B < 1 || H < 1 || S < 1 || SK < 1 || splits < 1) return 0;
+    return (int)(splits * kv_fill(B, H, S, SK, splits));
+}
 
 const char* fmha_mxfp8_version(void) { return "fmha_mxfp8 gfx950 1.0"; }
 
@@ -382,6 +401,9 @@ int fmha_mxfp8_launch_kvsplit(const fmha_mxfp8_kvsplit_args* a, uint32_t gx, uin
 int fmha_mxfp8_launch_combine(const fmha_mxfp8_combine_args* a, uint32_t gx, void* stream) {
     return launch_raw(K_COMBINE, a, sizeof(*a), gx, 1, 1, 256, stream, nullptr, 0);
 }
+int fmha_mxfp8_launch_combine_wide(const fmha_mxfp8_combine_args* a, uint32_t gx, void* stream) {
+    return launch_raw(K_COMBINE_WIDE, a, sizeof(*a), gx, 1, 1, 256, stream, nullptr, 0);
+}
 
 int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_t workspace_bytes, void* stream, int* path_out,
                               int* splits_out, char* err, size_t errlen) {
@@ -412,6 +434,8 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "v_seq32 must be 0 or 1");
     if (p->causal_pair < 0 || p->causal_pair > 2)
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "causal_pair must be 0, 1 or 2");
+    if (p->kv_fill != 0 && p->kv_fill != 1)
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "kv_fill must be 0 or 1");
     const bool scaled = p->softmax_scale != 0.0f;
     if (scaled && !scale_ok(p->softmax_scale))
         return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "softmax_scale must be 0 or positive with a normal f32 scale x log2(e)");
@@ -423,8 +447,15 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     std::memset(&sz, 0, sizeof(sz));
     sz.ptr_q = p->bytes_q; sz.ptr_k = p->bytes_k; sz.ptr_v = p->bytes_v; sz.ptr_o = p->bytes_o;
     sz.ptr_q_descale = p->bytes_q_descale; sz.ptr_k_descale = p->bytes_k_descale; sz.ptr_v_descale = p->bytes_v_descale;
+    // the KV split's partial count: the chunks times the fill, as far as the workspace holds it
+    i64 parts = splits;
+    if (path == FMHA_PATH_KVSPLIT) {
+        i64 sub = p->kv_fill ? 1 : kv_fill(B, H, S, SK, splits);
+        while (sub > 1 && workspace_bytes < fmha_mxfp8_workspace_bytes(B, H, S, (int)(splits * sub))) sub /= 2;
+        parts = splits * sub;
+    }
     if (path_out) *path_out = path;
-    if (splits_out) *splits_out = path == FMHA_PATH_KVSPLIT ? splits : 0;
+    if (splits_out) *splits_out = path == FMHA_PATH_KVSPLIT ? (int)parts : 0;
     const uint32_t gy = (uint32_t)H;
     if (path == FMHA_PATH_VS128 || path == FMHA_PATH_T128) {
         a.ptr_lse = p->lse;
@@ -460,7 +491,7 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     }
     // KV split: partials (fp32-sized rows, as ref_host.cpp:149 / ops.py:133) then the LSE, both in the workspace
     const i64 rows_total = B * S * H;
-    const size_t need = fmha_mxfp8_workspace_bytes(B, H, S, splits);
+    const size_t need = fmha_mxfp8_workspace_bytes(B, H, S, (int)parts);
     if (!workspace || workspace_bytes < need) {
         set_err(err, errlen, "GV-HOST-WORKSPACE: KV split needs %zu workspace bytes, got %zu", need, workspace_bytes);
         return FMHA_ERR_WORKSPACE;
@@ -475,17 +506,17 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     if (nslots > FMHA_WORKSPACE_SLOTS) nslots = FMHA_WORKSPACE_SLOTS;
     const size_t slot = nslots > 1 ? (size_t)(g_ws_turn.fetch_add(1, std::memory_order_relaxed) % nslots) : 0u;
     uint8_t* ohat = (uint8_t*)workspace + slot * stride;
-    uint8_t* lse = ohat + (size_t)splits * rows_total * 512;
+    uint8_t* lse = ohat + (size_t)parts * rows_total * 512;
     fmha_mxfp8_kvsplit_args ka;
     std::memcpy(&ka, &a, 0x270);
     ka.ptr_ohat = ohat;
     ka.ptr_lse = lse;
     const uint32_t part_fmt = p->f32_partials ? FMHA_KVS_F32_PARTIALS : 0u;
-    ka.kvs_splits = (uint32_t)splits | part_fmt | (p->v_seq32 ? FMHA_KVS_V_SEQ32 : 0u) | (scaled ? FMHA_KVS_SCALE : 0u);
+    ka.kvs_splits = (uint32_t)parts | part_fmt | (p->v_seq32 ? FMHA_KVS_V_SEQ32 : 0u) | (scaled ? FMHA_KVS_SCALE : 0u);
     ka.kvs_rows_total = (uint32_t)rows_total;
-    sz.ptr_ohat = (uint64_t)splits * rows_total * 512;
-    sz.ptr_lse = (uint64_t)splits * rows_total * 4;
-    const uint32_t gx = (uint32_t)((S + 255) / 256), gz = (uint32_t)(B * splits);
+    sz.ptr_ohat = (uint64_t)parts * rows_total * 512;
+    sz.ptr_lse = (uint64_t)parts * rows_total * 4;
+    const uint32_t gx = (uint32_t)((S + 255) / 256), gz = (uint32_t)(B * parts);
     int rc = p->no_check ? FMHA_OK : fmha_mxfp8_validate_kvsplit(&ka, &sz, gx, gy, gz, B, HK, 0, err, errlen);
     if (rc != FMHA_OK) return rc;
     rc = launch_raw(scaled ? K_KVSPLIT_SC : K_KVSPLIT, &ka, sizeof(ka), gx, gy, gz, 512, stream, err, errlen);
@@ -496,15 +527,18 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     ca.ptr_out = p->o;
     ca.rows_total = (uint32_t)rows_total;
     ca.d = 128;
-    ca.splits = (uint32_t)splits | part_fmt;
+    ca.splits = (uint32_t)parts | part_fmt;
     fmha_mxfp8_buffer_sizes csz = sz;
     csz.ptr_o = p->bytes_o;
     if (!p->no_check) {
         rc = fmha_mxfp8_validate_combine(&ca, &csz, 0, 1, 1, err, errlen);
         if (rc != FMHA_OK) return rc;
     }
-    const uint64_t cgrid = ((uint64_t)rows_total * 128 / 8 + 255) / 256;
-    return launch_raw(K_COMBINE, &ca, sizeof(ca), (uint32_t)(cgrid ? cgrid : 1), 1, 1, 256, stream, err, errlen);
+    // more than 8 partials per row: the combine with the splits spread over 4 waves (64 groups per block)
+    const bool wide = parts > 8;
+    const uint64_t cgrid = ((uint64_t)rows_total * 128 / 8 + (wide ? 63 : 255)) / (wide ? 64 : 256);
+    return launch_raw(wide ? K_COMBINE_WIDE : K_COMBINE, &ca, sizeof(ca), (uint32_t)(cgrid ? cgrid : 1), 1, 1, 256, stream, err,
+                      errlen);
 }
 
 }  // extern "C"

@@ -851,21 +851,33 @@ struct Wave {
 // The row sum of this lane's query (the ones pattern puts it in D dword (lane / 16) % 2).
 __device__ __forceinline__ float row_sum(const v4f& lacc, uint32_t lane) { return ((lane >> 4) & 1u) ? lacc[1] : lacc[0]; }
 
-// The LSE-weighted merge of the splits' partial rows (epilogue.rs:89-167) for NG groups: group t[g] is outputs
-// 8 (t & 15) .. +7 of partial row t >> 4, merged over splits 0 .. splits - 1 in order; out[g] receives the 8 bf16
-// results. F32: f32 partial rows (the extension) instead of fp16. For up to 8 splits every load of the NG groups is
-// issued before the first merge step, in one straight-line block with no branch: one memory latency per call (with a
-// branch per split on the row format, the compiler waited for each split's loads in turn).
-template <bool F32, int NG>
-__device__ __forceinline__ void combine_groups(const float* lse, const uint8_t* ohat, uint32_t rows, uint32_t splits,
-                                               const uint32_t (&t)[NG], v4i (&out)[NG]) {
+// The running state of the LSE-weighted merge (epilogue.rs:89-167) for 8 outputs of one row: base-2 maximum, weight
+// sum and the weighted sums.
+struct MergeState {
+    float m, den, acc[8];
+};
+
+__device__ __forceinline__ void merge_init(MergeState& st) {
+    st.m = -1.0e30f;
+    st.den = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[i] = 0.0f;
+}
+
+// st <- st merged with the splits lo .. hi - 1 (lo < hi), in order, for group t: outputs 8 (t & 15) .. +7 of partial
+// row t >> 4. F32: f32 partial rows (the extension) instead of fp16. The splits go in chunks of 8: every load of a
+// chunk is issued before its first merge step, in one straight-line block with no branch, so a chunk costs one memory
+// latency (with a branch per split on the row format, the compiler waited for each split's loads in turn).
+template <bool F32>
+__device__ __forceinline__ void merge_splits(const float* lse, const uint8_t* ohat, uint32_t rows, uint32_t lo, uint32_t hi,
+                                             uint32_t t, MergeState& st) {
     constexpr int NW = F32 ? 8 : 4;      // dwords of one split's 8 values
     // byte offsets below 2^32: validate refuses split partials of 4 GiB or more
     const __amdgpu_buffer_rsrc_t rl = make_rsrc(lse, 0xffffffffu), ro = make_rsrc(ohat, 0xffffffffu);
-    auto load = [&](uint32_t s, uint32_t tg, uint32_t& l, uint32_t (&xw)[NW]) {
-        const uint32_t r = s * rows + (tg >> 4);   // partial row index
+    auto load = [&](uint32_t s, uint32_t& l, uint32_t (&xw)[NW]) {
+        const uint32_t r = s * rows + (t >> 4);   // partial row index
         l = __builtin_amdgcn_raw_buffer_load_b32(rl, r * 4u, 0, 0);
-        const uint32_t off = ((r << 4) | (tg & 15u)) * (F32 ? 32u : 16u);
+        const uint32_t off = ((r << 4) | (t & 15u)) * (F32 ? 32u : 16u);
         const v4i x0 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, 0));
 #pragma unroll
         for (int i = 0; i < 4; ++i) xw[i] = (uint32_t)x0[i];
@@ -875,10 +887,7 @@ __device__ __forceinline__ void combine_groups(const float* lse, const uint8_t* 
             for (int i = 0; i < NW - 4; ++i) xw[4 + i] = (uint32_t)x1[i];
         }
     };
-    struct St {
-        float m, den, acc[8];
-    };
-    auto merge = [](St& st, float l, const uint32_t (&xw)[NW]) {
+    auto merge = [](MergeState& st, float l, const uint32_t (&xw)[NW]) {
         float x[8];
 #pragma unroll
         for (int i = 0; i < NW; ++i) {
@@ -894,44 +903,40 @@ __device__ __forceinline__ void combine_groups(const float* lse, const uint8_t* 
         for (int i = 0; i < 8; ++i) st.acc[i] = st.acc[i] * al + w * x[i];
         st.m = m_new;
     };
-    St st[NG];
+    // indices past hi re-read split hi - 1, which is not merged again
+    for (uint32_t s0 = lo; s0 < hi; s0 += 8u) {
+        uint32_t l[8], xw[8][NW];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        st[g].m = -1.0e30f;
-        st[g].den = 0.0f;
+        for (uint32_t s = 0; s < 8u; ++s) load(min(s0 + s, hi - 1u), l[s], xw[s]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) st[g].acc[i] = 0.0f;
+        for (uint32_t s = 0; s < 8u; ++s)
+            if (s0 + s < hi) merge(st, __builtin_bit_cast(float, l[s]), xw[s]);
     }
-    if (splits <= 8u) {
-        // indices past the split count re-read the last split, which is not merged
-        uint32_t l[NG][8], xw[NG][8][NW];
+}
+
+// a <- a merged with b (b covering splits after a's): the same weighting as one split's step, with b's weight sum and
+// weighted sums in place of one split's 1 and values.
+__device__ __forceinline__ void merge_states(MergeState& a, const MergeState& b) {
+    const float m_new = fmaxf(a.m, b.m);
+    const float dm = m_new * -1.0f;
+    const float al = __builtin_amdgcn_exp2f(a.m + dm);
+    const float w = __builtin_amdgcn_exp2f(b.m + dm);
+    a.den = a.den * al + b.den * w;
 #pragma unroll
-        for (int g = 0; g < NG; ++g)
+    for (int i = 0; i < 8; ++i) a.acc[i] = a.acc[i] * al + b.acc[i] * w;
+    a.m = m_new;
+}
+
+// the 8 bf16 results acc / den
+__device__ __forceinline__ v4i merge_finish(const MergeState& st) {
+    const float rd = __builtin_amdgcn_rcpf(st.den);
+    v4i out;
 #pragma unroll
-            for (uint32_t s = 0; s < 8u; ++s) load(min(s, splits - 1u), t[g], l[g][s], xw[g][s]);
-#pragma unroll
-        for (int g = 0; g < NG; ++g)
-#pragma unroll
-            for (uint32_t s = 0; s < 8u; ++s)
-                if (s < splits) merge(st[g], __builtin_bit_cast(float, l[g][s]), xw[g][s]);
-    } else {
-#pragma unroll
-        for (int g = 0; g < NG; ++g)
-            for (uint32_t s = 0; s < splits; ++s) {
-                uint32_t l, xw[NW];
-                load(s, t[g], l, xw);
-                merge(st[g], __builtin_bit_cast(float, l), xw);
-            }
+    for (int i = 0; i < 4; ++i) {
+        const v2bf w = {(__bf16)(st.acc[2 * i] * rd), (__bf16)(st.acc[2 * i + 1] * rd)};
+        out[i] = __builtin_bit_cast(int, w);
     }
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        const float rd = __builtin_amdgcn_rcpf(st[g].den);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const v2bf w = {(__bf16)(st[g].acc[2 * i] * rd), (__bf16)(st[g].acc[2 * i + 1] * rd)};
-            out[g][i] = __builtin_bit_cast(int, w);
-        }
-    }
+    return out;
 }
 
 // Epilogue. Full-sequence kernels: O = O^T . (v_descale / l) -> bf16 rows (state.rs:79-83); the optional natural-log
@@ -1542,9 +1547,57 @@ extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvspli
     t = t < groups ? t : groups - 1u;
     const float* lse = (const float*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_lse));
     const uint8_t* ohat = (const uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_ohat));
-    const uint32_t tg[1] = {t};
-    v4i outv[1];
-    if (split_field & FMHA_KVS_F32_PARTIALS) combine_groups<true, 1>(lse, ohat, rows, split_field & 0xffffu, tg, outv);
-    else combine_groups<false, 1>(lse, ohat, rows, split_field & 0xffffu, tg, outv);
-    *(v4i*)((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u) = outv[0];
+    const uint32_t splits = split_field & 0xffffu;
+    MergeState st;
+    merge_init(st);
+    if (split_field & FMHA_KVS_F32_PARTIALS) merge_splits<true>(lse, ohat, rows, 0u, splits, t, st);
+    else merge_splits<false>(lse, ohat, rows, 0u, splits, t, st);
+    *(v4i*)((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u) = merge_finish(st);
+}
+
+// Extension (no counterpart in the reference): the same merge for many splits, with the splits spread over the block's
+// 4 waves. Lane l of every wave takes group 64 blockIdx.x + l (outputs 8 (g & 15) .. +7 of row g >> 4, tail lanes redo
+// the last group); wave p merges the p-th quarter of the splits (ceil(splits / 4) each, in order), and wave 0 merges
+// the quarters in order through LDS. With the reference kernel's layout one thread walks every split of its group in
+// turn: at 32 splits that is 4 dependent rounds of loads on 64 groups per block (13.7 us at 1024 rows on MI355X).
+extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvsplit_combine_wide(fmha_mxfp8_combine_args a_) {
+    (void)a_;
+    __shared__ float part[3][10][64];
+    const uint32_t rows = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, rows_total));
+    const uint32_t split_field = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, splits));
+    const uint32_t splits = split_field & 0xffffu;
+    const uint32_t groups = rows << 4;
+    const uint32_t lane = threadIdx.x & 63u, p = threadIdx.x >> 6;
+    uint32_t t = blockIdx.x * 64u + lane;
+    t = t < groups ? t : groups - 1u;
+    const float* lse = (const float*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_lse));
+    const uint8_t* ohat = (const uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_ohat));
+    const uint32_t per = (splits + 3u) >> 2;
+    const uint32_t lo = min(p * per, splits), hi = min(lo + per, splits);
+    MergeState st;
+    merge_init(st);
+    if (lo < hi) {
+        if (split_field & FMHA_KVS_F32_PARTIALS) merge_splits<true>(lse, ohat, rows, lo, hi, t, st);
+        else merge_splits<false>(lse, ohat, rows, lo, hi, t, st);
+    }
+    if (p != 0u) {
+        part[p - 1][0][lane] = st.m;
+        part[p - 1][1][lane] = st.den;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) part[p - 1][2 + i][lane] = st.acc[i];
+    }
+    __syncthreads();
+    if (p != 0u) return;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        // a quarter past the split count (splits < 4) holds no split: skipped, so the result is the in-order merge
+        if ((uint32_t)(q + 1) * per >= splits) break;
+        MergeState o;
+        o.m = part[q][0][lane];
+        o.den = part[q][1][lane];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o.acc[i] = part[q][2 + i][lane];
+        merge_states(st, o);
+    }
+    *(v4i*)((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u) = merge_finish(st);
 }

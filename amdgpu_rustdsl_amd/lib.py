@@ -81,7 +81,7 @@ class Params(ctypes.Structure):
                 ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("HK", ctypes.c_int32), ("S", ctypes.c_int32), ("SK", ctypes.c_int32),
                 ("path", ctypes.c_int32), ("splits", ctypes.c_int32), ("causal", ctypes.c_int32),
                 ("f32_partials", ctypes.c_int32), ("v_seq32", ctypes.c_int32), ("softmax_scale", ctypes.c_float),
-                ("no_check", ctypes.c_int32), ("causal_pair", ctypes.c_int32)]
+                ("no_check", ctypes.c_int32), ("causal_pair", ctypes.c_int32), ("kv_fill", ctypes.c_int32)]
 
 
 assert ctypes.sizeof(Params) == 176 and ctypes.sizeof(Args) == 656 and ctypes.sizeof(KvsplitArgs) == 648 and ctypes.sizeof(CombineArgs) == 36
@@ -98,11 +98,13 @@ _L.fmha_mxfp8_fill_args.argtypes = [_P(Args), _vp, _vp, _vp, _vp, _vp, _vp, _vp,
 _L.fmha_mxfp8_fill_args.restype = None
 _L.fmha_mxfp8_workspace_bytes.argtypes = [_i64, _i64, _i64, _c]
 _L.fmha_mxfp8_workspace_bytes.restype = _sz
+_L.fmha_mxfp8_kv_partials.argtypes = [_i64, _i64, _i64, _i64, _c]
 _L.fmha_mxfp8_launch_vs128.argtypes = [_P(Args), _u32, _u32, _u32, _vp]
 _L.fmha_mxfp8_launch_t128.argtypes = [_P(Args), _u32, _u32, _u32, _vp]
 _L.fmha_mxfp8_launch_t128_split_tiles.argtypes = [_P(Args), _u32, _u32, _u32, _vp]
 _L.fmha_mxfp8_launch_kvsplit.argtypes = [_P(KvsplitArgs), _u32, _u32, _u32, _vp]
 _L.fmha_mxfp8_launch_combine.argtypes = [_P(CombineArgs), _u32, _vp]
+_L.fmha_mxfp8_launch_combine_wide.argtypes = [_P(CombineArgs), _u32, _vp]
 _L.fmha_fwd_hd128_mxfp8_auto.argtypes = [_P(Params), _vp, _sz, _vp, _P(_c), _P(_c), _cp, _sz]
 _L.fmha_fwd_hd128_mxfp8_auto_noalloc.argtypes = [_P(Params), _vp, _P(_c), _P(_c), _cp, _sz]
 _L.fmha_mxfp8_init.argtypes = [_cp, _sz]
@@ -116,8 +118,8 @@ _L.fmha_mxfp8_seq32_scale_bytes.argtypes = [_i64, _i64, _i64]
 _L.fmha_mxfp8_seq32_scale_bytes.restype = _sz
 
 EXPORTED = ["fmha_mxfp8_validate_vs128", "fmha_mxfp8_validate_t128", "fmha_mxfp8_validate_kvsplit", "fmha_mxfp8_validate_combine",
-            "fmha_mxfp8_select_path", "fmha_mxfp8_uses_split_tiles", "fmha_mxfp8_fill_args", "fmha_mxfp8_workspace_bytes", "fmha_mxfp8_launch_vs128",
-            "fmha_mxfp8_launch_t128", "fmha_mxfp8_launch_t128_split_tiles", "fmha_mxfp8_launch_kvsplit", "fmha_mxfp8_launch_combine", "fmha_fwd_hd128_mxfp8_auto",
+            "fmha_mxfp8_select_path", "fmha_mxfp8_uses_split_tiles", "fmha_mxfp8_fill_args", "fmha_mxfp8_workspace_bytes", "fmha_mxfp8_kv_partials", "fmha_mxfp8_launch_vs128",
+            "fmha_mxfp8_launch_t128", "fmha_mxfp8_launch_t128_split_tiles", "fmha_mxfp8_launch_kvsplit", "fmha_mxfp8_launch_combine", "fmha_mxfp8_launch_combine_wide", "fmha_fwd_hd128_mxfp8_auto",
             "fmha_fwd_hd128_mxfp8_auto_noalloc",
             "fmha_mxfp8_init", "fmha_mxfp8_version",
             "fmha_mxfp8_quantize_rows", "fmha_mxfp8_quantize_tensor", "fmha_mxfp8_quantize_seq32", "fmha_mxfp8_seq32_scale_bytes"]
@@ -155,6 +157,12 @@ def uses_split_tiles(path, B, H, S, SK, causal=False):
 
 def workspace_bytes(B, H, S, splits):
     return int(_L.fmha_mxfp8_workspace_bytes(B, H, S, splits))
+
+
+def kv_partials(B, H, S, SK, splits):
+    """Partials per row the one-call entry writes for a KV split of ``splits`` chunks when the workspace holds them
+    (the chunks times the fill that spreads each chunk over up to 8 blocks; the current device's CU count)."""
+    return int(_L.fmha_mxfp8_kv_partials(B, H, S, SK, splits))
 
 
 def fill_args(o, q, k, v, qs, ks, vs, B, H, HK, S, SK):

@@ -53,8 +53,9 @@ def _ws(device, stream, nbytes):
 
 
 def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", splits=None, specialize=True, stream=None, check=True,
-                   lse=None, causal=False, partials="fp16", softmax_scale=None, causal_pair="auto"):
-    """Attention forward on MXFP8 inputs with head dim 128, written into ``out``; returns the (path, splits) that ran.
+                   lse=None, causal=False, partials="fp16", softmax_scale=None, causal_pair="auto", kv_fill=True):
+    """Attention forward on MXFP8 inputs with head dim 128, written into ``out``; returns the (path, splits) that ran
+    (for the KV split, the partials per row: the chunks times the blocks each chunk was spread over).
 
     Scores are base-2: the kernels compute softmax2(q . k) over dequantised q and k, so a caller that wants the usual
     softmax(q k^T / sqrt(128)) multiplies q by log2(e) / sqrt(128) before quantising it (``fmha_fwd_bf16_via_mxfp8``
@@ -75,7 +76,10 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     ``causal`` masks key t from query i unless t <= i + SK - S; ``partials="fp32"`` keeps the KV split's partial rows
     in float32; ``softmax_scale`` makes the kernel apply scale * log2(e) to q . k itself (q then quantised unscaled);
     ``causal_pair`` ("auto", True, False): with ``causal``, one block runs query tiles x and T - 1 - x, so that every block
-    has the same work; "auto" pairs when the unpaired grid exceeds the device's CUs (same output bits either way).
+    has the same work; "auto" pairs when the unpaired grid exceeds the device's CUs (same output bits either way);
+    ``kv_fill`` (default True): a KV split whose grid would leave CUs idle spreads each chunk's keys over up to 8
+    blocks (``lib.kv_partials``), the combine merging every block's partial; False keeps the reference's one block
+    per chunk.
     """
     pair_modes = {"auto": 0, True: 1, False: 2}
     if causal_pair not in pair_modes:
@@ -123,6 +127,7 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     p.v_seq32 = int(v_seq32)
     p.no_check = int(not check)
     p.causal_pair = pair_modes[causal_pair]
+    p.kv_fill = 0 if kv_fill else 1
     if softmax_scale is not None:
         if not float(softmax_scale) > 0.0:
             raise ValueError(f"fmha_fwd_mxfp8: softmax_scale must be positive, got {softmax_scale!r}")
@@ -131,7 +136,9 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     want_path, want_splits = (select_path(B, H, S, SK) if path_id < 0 else (path, nsplit))
     ws, ws_bytes = None, 0
     if want_path == "kvsplit" and not causal:
-        ws_bytes = lib.workspace_bytes(B, H, S, want_splits)
+        # the entry's partials: the chunks, each spread over up to 8 blocks when the grid would leave CUs idle
+        parts = lib.kv_partials(B, H, S, SK, want_splits) if kv_fill else want_splits
+        ws_bytes = lib.workspace_bytes(B, H, S, parts)
         # room for the entry's workspace slots (consecutive calls then write partials the previous combine did not
         # just read), unless that would take more than 512 MiB
         slotted = lib.WORKSPACE_SLOTS * ((ws_bytes + 255) // 256 * 256)

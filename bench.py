@@ -145,7 +145,8 @@ def main():
     p.B, p.H, p.HK, p.S, p.SK = B, H, HK, S, SK
     p.path = -1 if path == "auto" else lib.PATH_IDS[path]
     p.splits, p.causal = splits or 0, int(causal)
-    ws_bytes = lib.workspace_bytes(B, H, S, used[1]) if used[0] == "kvsplit" else 0
+    # the KV split's workspace as the op sizes it: the entry's workspace slots of the partials that ran
+    ws_bytes = lib.WORKSPACE_SLOTS * ((lib.workspace_bytes(B, H, S, used[1]) + 255) // 256 * 256) if used[0] == "kvsplit" else 0
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     st = stream.cuda_stream
 
@@ -235,7 +236,7 @@ def main():
         "dtype": "e4m3 (MXFP8, E8M0/32 scales, fp32 accumulate)",
         "data": "synthetic: N(0,1) Q/K/V quantised to MXFP8 like the reference's REF_DATA=normal generator, drawn on the GPU",
         "config": {"workload": f"fmha_fwd_hd128_mxfp8_auto {desc}", "B": B, "H": H, "HK": HK, "S": S, "SK": SK,
-                   "causal": causal, "path": used[0], "splits": used[1], "lse": lse is not None,
+                   "causal": causal, "path": used[0], "splits": used[1], "kv_chunks": (splits or lib.select_path(B, H, S, SK)[1]) if used[0] == "kvsplit" else None, "lse": lse is not None,
                    "pct_mxfp8_peak": round(100 * tflops / PEAK_MXFP8_TFLOPS, 2)},
         "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": PEAK_MXFP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(kern_tflops / PEAK_MXFP8_TFLOPS, 4), "traffic": traffic,

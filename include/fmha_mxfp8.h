@@ -223,6 +223,13 @@ void fmha_mxfp8_fill_args(fmha_mxfp8_args* a, void* o, const void* q, const void
 /* KV-split workspace bytes: fp32-sized partial rows + LSE (ref_host.cpp:146-149, ops.py:133-134). */
 size_t fmha_mxfp8_workspace_bytes(int64_t B, int64_t H, int64_t S, int splits);
 
+/* Extension (no counterpart in the reference): the number of partials per row that fmha_fwd_hd128_mxfp8_auto writes
+ * for a KV split of `splits` chunks when its workspace holds them: each chunk's key range is divided into sub = 1, 2,
+ * 4 or 8 consecutive ranges, sub doubling while the grid ((S + 255) / 256 x H x B x splits x sub blocks) stays within
+ * the device's CU count and every range keeps at least 4 key tiles. Returns splits x sub (0 for invalid sizes). The
+ * workspace for it is fmha_mxfp8_workspace_bytes(B, H, S, fmha_mxfp8_kv_partials(...)). */
+int fmha_mxfp8_kv_partials(int64_t B, int64_t H, int64_t S, int64_t SK, int splits);
+
 /* ------------------------------------------------------------------------- */
 /* Launch                                                                    */
 /* ------------------------------------------------------------------------- */
@@ -239,6 +246,11 @@ int fmha_mxfp8_launch_t128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, u
 int fmha_mxfp8_launch_t128_split_tiles(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream);
 int fmha_mxfp8_launch_kvsplit(const fmha_mxfp8_kvsplit_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream);
 int fmha_mxfp8_launch_combine(const fmha_mxfp8_combine_args* a, uint32_t gx, void* stream);
+/* Extension (no counterpart in the reference): the same merge on fmha_fwd_hd128_mxfp8_v3_kvsplit_combine_wide, which
+ * spreads each row's splits over a block's 4 waves (quarters merged in order): 64 groups of 8 outputs per block, grid
+ * gx = ceil(rows_total x 16 / 64), 256 threads. Same arguments and rules as the combine; the one-call entry runs it
+ * for more than 8 partials per row. */
+int fmha_mxfp8_launch_combine_wide(const fmha_mxfp8_combine_args* a, uint32_t gx, void* stream);
 
 /* Problem description of the one-call entry. All pointers are device pointers
  * to packed tensors (layouts in fmha_mxfp8_args). */
@@ -251,7 +263,7 @@ typedef struct fmha_mxfp8_params {
     uint64_t bytes_q_descale, bytes_k_descale, bytes_v_descale;
     int32_t B, H, HK, S, SK;
     int32_t path;              /* -1 = auto (dispatch rule), else FMHA_PATH_* */
-    int32_t splits;            /* KV split count when path == FMHA_PATH_KVSPLIT (2, 4 or 8; 0 = 4) */
+    int32_t splits;            /* KV split chunks when path == FMHA_PATH_KVSPLIT (2, 4 or 8; 0 = 4) */
     int32_t causal;            /* 0 = the reference semantics; 1 = bottom-right causal mask (extension) */
     int32_t f32_partials;      /* KV split only: 0 = fp16 partial rows (the reference's); 1 = f32 (extension) */
     int32_t v_seq32;           /* 0 = v_descale is one f32 (the reference's); 1 = E8M0 per 32 keys per column (extension) */
@@ -262,6 +274,9 @@ typedef struct fmha_mxfp8_params {
                                   vouches for the buffer extents and strides */
     int32_t causal_pair;       /* causal only (extension): 0 = the causal q-tile pairing (FMHA_FLAG_CAUSAL_PAIR) when
                                   the unpaired grid has more blocks than the device has CUs; 1 = always; 2 = never */
+    int32_t kv_fill;           /* KV split only (extension): 0 = each chunk spread over the blocks that
+                                  fmha_mxfp8_kv_partials names, as far as the workspace holds their partials;
+                                  1 = the reference's chunks only (one block per chunk and query tile) */
 } fmha_mxfp8_params;
 
 /* fmha_fwd_hd128_mxfp8_auto: dispatch + validate + launch (+ combine), all on

@@ -173,7 +173,9 @@ def emulate(inp, splits=0, rows=64, threads=0, partials=False, f32_partials=Fals
     Returns the bf16 output (uint16, rows not emulated are 0), and with ``partials`` also (ohat, lse f32): ohat fp16
     (uint16), or f32 with ``f32_partials`` (the FMHA_KVS_F32_PARTIALS extension). ``split_tiles`` models the library's
     order (two 64-key streams per tile, merged; not with the LUT recipe) instead of the reference's: for KV-split blocks
-    of at most 128 query rows, and with ``splits=0`` for every row (the t128 path's split-tile kernel)."""
+    of at most 128 query rows, and with ``splits=0`` for every row (the t128 path's split-tile kernel). At most 64
+    splits."""
+    assert 0 <= splits <= 64, f"emulate: {splits} splits (at most 64)"
     out = np.zeros(inp.out_elems, np.uint16)
     if not isinstance(rows, (int, np.integer)):
         assert not partials, "partials are emulated for leading rows only"

@@ -675,8 +675,8 @@ static void emu_item(const void* vctx, long item) {
     }
     const long rows_total = (long)p->B * p->S * p->H;
     const long prow = ((long)b * p->S + i) * p->H + h;
-    float lse_s[8];
-    float oh[8][D];      /* the partial row as stored (fp16-rounded unless f32_partials) */
+    float lse_s[MXO_MAX_SPLITS];
+    float oh[MXO_MAX_SPLITS][D];      /* the partial row as stored (fp16-rounded unless f32_partials) */
     for (int s = 0; s < c->splits; ++s) {
         int key_lo, kv_eff;
         mxo_split_range(p->SK, c->splits, s, &key_lo, &kv_eff);
@@ -728,6 +728,7 @@ static void emu_item(const void* vctx, long item) {
 
 void mxo_emulate_ex(const mxo_problem* p, int splits, int rows, uint16_t* out_bf16, void* ohat, float* lse_f32,
                     int f32_partials, int split_tiles, int threads) {
+    if (splits > MXO_MAX_SPLITS) return;   /* refused (the Python wrapper checks first) */
     if (rows <= 0 || rows > p->S) rows = p->S;
     emu_ctx c = {p, splits, rows, out_bf16, ohat, lse_f32, f32_partials, split_tiles, NULL};
     run_parallel(threads, (long)p->B * p->H * rows, &c, emu_item);
@@ -735,6 +736,7 @@ void mxo_emulate_ex(const mxo_problem* p, int splits, int rows, uint16_t* out_bf
 
 void mxo_emulate_rows(const mxo_problem* p, int splits, const int* row_list, int rows, uint16_t* out_bf16, int f32_partials,
                       int split_tiles, int threads) {
+    if (splits > MXO_MAX_SPLITS) return;   /* refused (the Python wrapper checks first) */
     emu_ctx c = {p, splits, rows, out_bf16, NULL, NULL, f32_partials, split_tiles, row_list};
     run_parallel(threads, (long)p->B * p->H * rows, &c, emu_item);
 }

@@ -118,6 +118,8 @@ void mxo_combine(const uint16_t* ohat_f16, const float* lse, uint16_t* out_bf16,
  * (two 64-key streams per tile, merged; non-LUT recipe only) for KV-split blocks of at most 128 query rows, and,
  * with splits = 0, for every row (the t128 path's split-tile kernel).
  * mxo_emulate is mxo_emulate_ex(..., 0, 0, ...). */
+/* at most MXO_MAX_SPLITS splits (more: nothing is written) */
+#define MXO_MAX_SPLITS 64
 void mxo_emulate_ex(const mxo_problem* p, int splits, int rows, uint16_t* out_bf16, void* ohat, float* lse_f32,
                     int f32_partials, int split_tiles, int threads);
 /* mxo_emulate_ex (no partials out) over the query rows row_list[0 .. nrows) of every (b, h). */

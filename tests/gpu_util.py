@@ -3,7 +3,7 @@ import numpy as np
 import torch
 
 import oracle
-from amdgpu_rustdsl_amd import ops
+from amdgpu_rustdsl_amd import lib, ops
 
 D = 128
 
@@ -26,7 +26,18 @@ def upload(inp, device):
     return q, k, v, qs, ks, vs
 
 
-def run(inp, device, path="auto", splits=None, lse=False, poison=True, partials="fp16", causal_pair="auto"):
+def chunks(inp, path="auto", splits=None):
+    """The reference's KV-split chunk count for a run of `path` (0 when the run is not a KV split): the forced count,
+    or the dispatch's."""
+    if path == "kvsplit":
+        return splits or 4
+    if path == "auto" and not inp.causal:
+        p, sp = lib.select_path(inp.B, inp.H, inp.S, inp.SK)
+        return sp if p == "kvsplit" else 0
+    return 0
+
+
+def run(inp, device, path="auto", splits=None, lse=False, poison=True, partials="fp16", causal_pair="auto", kv_fill=True):
     """Runs the op; returns (bf16 output as uint16 numpy [B*S*H*128], (path, splits), lse tensor or None)."""
     q, k, v, qs, ks, vs = upload(inp, device)
     out = torch.empty(inp.B, inp.S, inp.H, D, dtype=torch.bfloat16, device=device)
@@ -35,7 +46,7 @@ def run(inp, device, path="auto", splits=None, lse=False, poison=True, partials=
     lse_t = torch.full((inp.B, inp.H, inp.S), float("nan"), dtype=torch.float32, device=device) if lse else None
     used = ops.fmha_fwd_mxfp8(q, k, v, qs, ks, vs, out, path=path, splits=splits, lse=lse_t, causal=inp.causal,
                               partials=partials, softmax_scale=inp.qk_scale if inp.qk_scale > 0 else None,
-                              causal_pair=causal_pair)
+                              causal_pair=causal_pair, kv_fill=kv_fill)
     torch.cuda.synchronize()
     o = out.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
     return o, used, lse_t

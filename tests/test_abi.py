@@ -264,6 +264,7 @@ def _params(**kw):
     p = lib.Params()
     p.B, p.H, p.HK, p.S, p.SK = kw.get("B", 1), kw.get("H", 8), kw.get("HK", 8), kw.get("S", 128), kw.get("SK", 4096)
     p.path, p.splits, p.causal = kw.get("path", -1), kw.get("splits", 0), kw.get("causal", 0)
+    p.kv_fill = kw.get("kv_fill", 0)
     big = 1 << 40
     p.o = p.q = p.k = p.v = p.q_descale = p.k_descale = p.v_descale = 0x1000
     p.bytes_q = p.bytes_k = p.bytes_v = p.bytes_o = p.bytes_q_descale = p.bytes_k_descale = p.bytes_v_descale = big
@@ -278,6 +279,7 @@ def _params(**kw):
     (dict(path=2, splits=3), lib.FMHA_ERR_PATH),            # splits not in {2, 4, 8}
     (dict(path=2, splits=8, SK=4224), lib.FMHA_ERR_PATH),   # 33 tiles, 5 per split: split 7 would start past the end
     (dict(path=2, splits=4, causal=1), lib.FMHA_ERR_PATH),  # no causal on the KV split
+    (dict(kv_fill=2), lib.FMHA_ERR_KA_RANGE),               # kv_fill is 0 or 1
 ])
 def test_auto_rejects_before_any_gpu_work(kw, code):
     """fmha_fwd_hd128_mxfp8_auto checks its arguments before touching the device (these run without a GPU)."""
@@ -413,3 +415,21 @@ def test_causal_pair_flag_rules():
     assert lib.uses_split_tiles("vs128", 4, 8, 2048, 2048, causal=True)
     assert not lib.uses_split_tiles("vs128", 4, 8, 2048, 2048, causal=False)
     assert not lib.uses_split_tiles("vs128", 4, 8, 2048, 384, causal=True)
+
+
+@pytest.mark.parametrize("shape,chunks,parts", [
+    ((1, 8, 128, 16384), 8, 32),     # config 5: 8 blocks per chunk -> 64, spread 4 ways -> 256 blocks of 4 key tiles
+    ((1, 8, 128, 16000), 8, 16),     # 125 key tiles: 32 ranges would leave fewer than 4 tiles each
+    ((1, 8, 128, 16384), 4, 32),     # the dispatch's 4 chunks: spread 8 ways (the most)
+    ((1, 8, 2048, 2048), 4, 4),      # 256 blocks already
+    ((1, 8, 512, 32768), 4, 16),     # 64 blocks -> 256
+    ((1, 8, 512, 4096), 4, 8),       # 32 key tiles: 8 ranges of 4
+    ((1, 8, 64, 1000), 2, 2),        # 8 key tiles: 2 ranges of 4 already
+    ((1, 8, 2048, 2048), 8, 8),      # 512 blocks: beyond the CUs, no spread
+    ((0, 8, 128, 4096), 4, 0),       # invalid sizes
+])
+def test_kv_partials_rule(shape, chunks, parts):
+    """fmha_mxfp8_kv_partials (extension): chunks x sub, sub = 1, 2, 4 or 8 doubling while (S + 255) / 256 H B chunks
+    sub blocks stay within the CU count (256 on MI355X; the value the library assumes without a device) and every
+    key range keeps at least 4 key tiles."""
+    assert lib.kv_partials(*shape, chunks) == parts

@@ -59,16 +59,18 @@ class _Emu:
 
 
 def _run_path(gpu, inp, path):
-    """Runs `path`; returns (output, (splits, split_tiles) of the order it computes in, what ran)."""
+    """Runs `path`; returns (output, (splits, split_tiles) of the order it computes in, what ran, the reference's KV
+    chunks on that path: 0 unless it is a KV split)."""
     B, H, S, SK = inp.B, inp.H, inp.S, inp.SK
     if path == "vs128_direct":
-        return gpu_util.run_direct(inp, gpu, "vs128"), (0, False), "fmha_fwd_hd128_mxfp8_v3_vs128 (512 threads)"
+        return gpu_util.run_direct(inp, gpu, "vs128"), (0, False), "fmha_fwd_hd128_mxfp8_v3_vs128 (512 threads)", 0
     if path == "t128_direct":
-        return gpu_util.run_direct(inp, gpu, "t128"), (0, False), "fmha_fwd_hd128_mxfp8_v3_t128 (256 threads)"
-    out, used, _ = gpu_util.run(inp, gpu, path=path, splits=2 if path == "kvsplit" else None)
+        return gpu_util.run_direct(inp, gpu, "t128"), (0, False), "fmha_fwd_hd128_mxfp8_v3_t128 (256 threads)", 0
+    splits = 2 if path == "kvsplit" else None
+    out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
     if used[0] == "kvsplit":
-        return out, (used[1], True), used
-    return out, (0, lib.uses_split_tiles(used[0], B, H, S, SK, inp.causal)), used
+        return out, (used[1], True), used, gpu_util.chunks(inp, path, splits)
+    return out, (0, lib.uses_split_tiles(used[0], B, H, S, SK, inp.causal)), used, 0
 
 
 # A score's MFMA error bound, relative to the sum of its product magnitudes: what the hardware fixture allows
@@ -107,8 +109,8 @@ def test_run_ref_gate(gpu, shape, mode):
             with pytest.raises(lib.FmhaError, match="GV-HOST-PATH"):
                 gpu_util.run(inp, gpu, path="kvsplit", splits=2)
             continue
-        out, order, used = _run_path(gpu, inp, path)
-        ref_emu = emu.get(order[0], False)   # the reference's kernels on the same path (their order)
+        out, order, used, ref_chunks = _run_path(gpu, inp, path)
+        ref_emu = emu.get(ref_chunks, False)   # the reference's kernels on the same path (their order and chunks)
         stats = oracle.check_fp64(inp, out, rows=rows)
         ref = oracle.check_fp64(inp, ref_emu, rows=rows)
         cmp = gpu_util.compare_to_emulation(out, emu.get(*order), inp, rows)
@@ -190,11 +192,11 @@ def test_split_vs_full(gpu, case):
     rows = oracle.first_and_last(S, 64)
     full = gpu_util.run_direct(inp, gpu, "vs128")
     split, used, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits)
-    assert used == ("kvsplit", splits)
+    assert used == ("kvsplit", lib.kv_partials(B, H, S, SK, splits))
     sel = lambda x: x.reshape(B, S, H, 128)[:, rows]
     ours = _diff(sel(split), sel(full))
     emu_full = oracle.emulate(inp, rows=rows)
-    emu_split = oracle.emulate(inp, splits=splits, rows=rows, split_tiles=True)
+    emu_split = oracle.emulate(inp, splits=used[1], rows=rows, split_tiles=True)
     emu_ref_split = oracle.emulate(inp, splits=splits, rows=rows)
     want = _diff(sel(emu_split), sel(emu_full))          # the same pair of orders, emulated
     ref = _diff(sel(emu_ref_split), sel(emu_full))       # the reference kernels' pair

@@ -38,12 +38,14 @@ CASES = [
 ]
 
 
-def _emulated_bar(inp, splits, rows=ROWS, path=None, **kw):
-    """The reference's error statistics (its order), and the emulation to compare element-wise with: the library's
-    own order, which differs from the reference's for KV-split blocks of at most 128 query rows and where the one-call
-    entry runs a full-sequence path on the split-tile kernel (lib.uses_split_tiles; not with the LUT recipe, which
-    the emulation handles)."""
-    emu = oracle.emulate(inp, splits=splits, rows=rows, **kw)
+def _emulated_bar(inp, splits, rows=ROWS, path=None, ref_splits=None, **kw):
+    """The reference's error statistics (its order, on its `ref_splits` KV chunks, default `splits`), and the
+    emulation to compare element-wise with: the library's own order on the `splits` partials that ran (the chunks
+    times the blocks each was spread over), which also differs from the reference's for KV-split blocks of at most
+    128 query rows and where the one-call entry runs a full-sequence path on the split-tile kernel
+    (lib.uses_split_tiles; not with the LUT recipe, which the emulation handles)."""
+    ref_splits = splits if ref_splits is None else ref_splits
+    emu = oracle.emulate(inp, splits=ref_splits, rows=rows, **kw)
     ref_stats = oracle.check_fp64(inp, emu, rows=rows)
     if splits or (path is not None and lib.uses_split_tiles(path, inp.B, inp.H, inp.S, inp.SK, inp.causal)):
         emu = oracle.emulate(inp, splits=splits, rows=rows, split_tiles=True, **kw)
@@ -59,7 +61,7 @@ def test_parity(gpu, case):
     used_splits = used[1] if used[0] == "kvsplit" else 0
     # the reference's sample (the first 64 rows of every (b, h)) and the last 64: the last query tile and the tail
     rows = oracle.first_and_last(S, ROWS)
-    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0])
+    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0], ref_splits=gpu_util.chunks(inp, path, splits))
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
     print(f"[case] {name} path={used} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
@@ -123,9 +125,9 @@ def test_parity_f32_partials(gpu, case):
     print(f"[case] f32 partials {name}", flush=True)
     inp = oracle.Inputs(B, H, S, SK, HK=HK)
     out, used, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits, partials="fp32")
-    assert used == ("kvsplit", splits)
+    assert used == ("kvsplit", lib.kv_partials(B, H, S, SK, splits))
     out16, _, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits)
-    emu, ref_stats = _emulated_bar(inp, splits, f32_partials=True)
+    emu, ref_stats = _emulated_bar(inp, used[1], f32_partials=True, ref_splits=splits)
     stats = oracle.check_fp64(inp, out, rows=ROWS)
     stats16 = oracle.check_fp64(inp, out16, rows=ROWS)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, min(ROWS, S))
@@ -159,7 +161,7 @@ def test_parity_v_seq32(gpu, case):
     assert used[0] == path
     used_splits = used[1] if used[0] == "kvsplit" else 0
     rows = oracle.first_and_last(S, 128 if causal else ROWS)
-    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0])
+    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0], ref_splits=gpu_util.chunks(inp, path, splits))
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
     print(f"[case] v_seq32 {name} path={used} ours={stats} emulated={ref_stats} vs-emulation={cmp}", flush=True)
@@ -215,8 +217,8 @@ def test_parity_split_tiles(gpu, case):
     inp = oracle.Inputs(B, H, S, SK, HK=HK, v_seq32=opt.get("v_seq32", False))
     f32 = opt.get("partials") == "fp32"
     out, used, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits, partials=opt.get("partials", "fp16"))
-    assert used == ("kvsplit", splits)
-    emu, ref_stats = _emulated_bar(inp, splits, rows=S, f32_partials=f32)
+    assert used == ("kvsplit", lib.kv_partials(B, H, S, SK, splits))
+    emu, ref_stats = _emulated_bar(inp, used[1], rows=S, f32_partials=f32, ref_splits=splits)
     stats = oracle.check_fp64(inp, out, rows=S)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, S)
     print(f"[case] split tiles {name} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
@@ -251,7 +253,7 @@ def test_parity_qk_scale(gpu, case):
     assert used[0] == path
     used_splits = used[1] if used[0] == "kvsplit" else 0
     rows = S if path == "kvsplit" else oracle.first_and_last(S, 128 if causal else ROWS)
-    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0])
+    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0], ref_splits=gpu_util.chunks(inp, path, splits))
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
     print(f"[case] qk scale {name} path={used} ours={stats} emulated={ref_stats} vs-emulation={cmp}", flush=True)
@@ -406,6 +408,8 @@ def test_workspace_slots(gpu):
     B, H, S, SK = inp.B, inp.H, inp.S, inp.SK
     used = lib.select_path(B, H, S, SK)
     assert used[0] == "kvsplit"
+    # (sized for the partials the entry writes with the fill, so that every workspace below runs the same partials)
+    used = (used[0], lib.kv_partials(B, H, S, SK, used[1]))
     need = lib.workspace_bytes(B, H, S, used[1])
     st = torch.cuda.current_stream(gpu).cuda_stream
 
@@ -429,3 +433,40 @@ def test_workspace_slots(gpu):
     four = torch.full((lib.WORKSPACE_SLOTS * stride,), 0xFF, dtype=torch.uint8, device=gpu)
     for i in range(2 * lib.WORKSPACE_SLOTS + 1):
         np.testing.assert_array_equal(call(four, four.numel()), want, err_msg=f"call {i}")
+
+
+# Extension: the KV-split fill. With few blocks per chunk the one-call entry spreads each of the reference's chunks
+# over up to 8 blocks (lib.kv_partials) and merges every block's partial (the combine with the splits spread over a
+# block's 4 waves above 8 partials per row). Bar: the reference's statistics on its own chunks, and element-wise
+# closeness to the emulation of the partials that ran; kv_fill=False runs the reference's chunks only.
+FILL_CASES = [
+    ("cfg5_B1H8S128_SK16384_split8", 1, 8, 8, 128, 16384, "kvsplit", 8),
+    ("cfg5_tail_B1H8S128_SK16000_split8", 1, 8, 8, 128, 16000, "kvsplit", 8),
+    ("auto_B1H8S512_SK32768", 1, 8, 8, 512, 32768, "auto", None),
+    ("auto_gqa4_B1H8HK2_S256_SK8192", 1, 8, 2, 256, 8192, "auto", None),
+]
+
+
+@pytest.mark.parametrize("case", FILL_CASES, ids=[c[0] for c in FILL_CASES])
+def test_parity_kv_fill(gpu, case):
+    name, B, H, HK, S, SK, path, splits = case
+    print(f"[case] kv fill {name}", flush=True)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK)
+    chunks = gpu_util.chunks(inp, path, splits)
+    out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
+    ref_out, ref_used, _ = gpu_util.run(inp, gpu, path=path, splits=splits, kv_fill=False)
+    assert used == ("kvsplit", lib.kv_partials(B, H, S, SK, chunks)) and used[1] > chunks
+    assert ref_used == ("kvsplit", chunks)
+    rows = oracle.first_and_last(S, ROWS)
+    emu, ref_stats = _emulated_bar(inp, used[1], rows=rows, ref_splits=chunks)
+    stats = oracle.check_fp64(inp, out, rows=rows)
+    stats_chunks = oracle.check_fp64(inp, ref_out, rows=rows)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
+    print(f"[case] kv fill {name} ran={used} ours={stats} chunks-only={stats_chunks} emulated-reference={ref_stats} "
+          f"vs-emulation={cmp}", flush=True)
+    assert not np.isnan(oracle.bf16_to_f32(out)).any()
+    for st in (stats, stats_chunks):
+        assert st["bad"] <= ref_stats["bad"]
+        assert st["mean_err"] <= 1.10 * ref_stats["mean_err"]
+    assert cmp["mean_abs"] <= 0.6 * ref_stats["mean_err"], cmp
+    assert cmp["max_abs"] <= 0.05, cmp

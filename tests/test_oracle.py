@@ -310,25 +310,27 @@ def test_emulation_deterministic():
     np.testing.assert_array_equal(a, b)
 
 
-@pytest.mark.parametrize("splits", [2, 4, 8])
+@pytest.mark.parametrize("splits", [2, 4, 8, 16, 32])
 def test_split_matches_full_statistically(splits):
     """Each KV split starts its own softmax reference (b = 64), so its fp8 P rounding differs from the full-sequence
-    kernel's and the outputs differ at the quantisation-noise level, not bit for bit: the split output must be as
-    accurate as the full one (fp64 check) and differ from it by less than that error."""
+    kernel's and the outputs differ at the quantisation-noise level, not bit for bit: the split output must be at
+    least as accurate as the full one (fp64 check) and differ from it by less than that error."""
     inp = oracle.Inputs(1, 2, 64, 4096 - 50)
     full_o = oracle.emulate(inp, splits=0, rows=64)
     sp_o = oracle.emulate(inp, splits=splits, rows=64)
     st_full, st_sp = oracle.check_fp64(inp, full_o, rows=64), oracle.check_fp64(inp, sp_o, rows=64)
-    assert st_sp["bad"] == 0 and abs(st_sp["mean_err"] / st_full["mean_err"] - 1) < 0.1
+    # (no less accurate; splits of fewer than 4 key tiles take the exact-rebasing recipe and come out more accurate)
+    assert st_sp["bad"] == 0 and st_sp["mean_err"] / st_full["mean_err"] < 1.1
     diff = np.abs(oracle.bf16_to_f32(full_o).astype(np.float64) - oracle.bf16_to_f32(sp_o))
     assert diff.mean() < 1.5 * st_full["mean_err"] * (inp.S / 64)
 
 
-def test_combine_closed_form():
+@pytest.mark.parametrize("splits", [4, 32])
+def test_combine_closed_form(splits):
     """epilogue.rs:89-167 streaming merge == the closed form sum_s 2^lse_s O_s / sum_s 2^lse_s (to bf16 rounding);
     a split with lse = -1e30 (no keys) has weight 0."""
     rng = np.random.default_rng(11)
-    rows, splits = 37, 4
+    rows = 37
     ohat = rng.standard_normal((splits, rows, D)).astype(np.float16)
     lse = (rng.standard_normal((splits, rows)) * 6 - 3).astype(np.float32)
     lse[2, 5] = -1e30

@@ -34,7 +34,9 @@ def _both(gpu, inp, path=-1, splits=0):
     out_na = torch.full_like(out_ref, float("nan"))
     p = _params(inp, tensors, out_ref, path, splits)
     used = lib.select_path(inp.B, inp.H, inp.S, inp.SK) if path < 0 else (lib.PATH_NAMES[path], splits)
-    ws_bytes = lib.workspace_bytes(inp.B, inp.H, inp.S, used[1]) if used[0] == "kvsplit" else 0
+    # (sized for the partials of the chunk fill, as the scratch array holds them: both entries then run the same)
+    parts = lib.kv_partials(inp.B, inp.H, inp.S, inp.SK, used[1]) if used[0] == "kvsplit" else 0
+    ws_bytes = lib.workspace_bytes(inp.B, inp.H, inp.S, parts) if used[0] == "kvsplit" else 0
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=gpu)
     got_ref = lib.run_auto(p, ws.data_ptr(), ws_bytes, st)
     p.o = out_na.data_ptr()
