@@ -146,6 +146,31 @@ __device__ inline T ka(uint32_t off) {
 }
 #define KA_FIELD(T, field) ka<T>(offsetof(fmha_mxfp8_args, field))
 
+// The kernel arguments span ten 64-byte lines (0x000-0x28F), and the segment is fresh from the host for every launch,
+// so every line misses the caches. Left to itself the compiler reads the fields in three dependent batches (it spills
+// some into VGPR lanes between them), each batch touching new lines: three memory round trips before the first tile
+// load. One scalar load per line, all in flight together and waited for once, brings every line into the scalar cache
+// in a single round trip; the field reads that follow hit it. (Scalar loads only: nothing is written.)
+__device__ __forceinline__ void kernarg_lines_touch() {
+    uint32_t t0, t1, t2, t3, t4, t5, t6, t7, t8, t9;
+    asm volatile(
+        "s_load_dword %0, %10, 0x0\n\t"
+        "s_load_dword %1, %10, 0x40\n\t"
+        "s_load_dword %2, %10, 0x80\n\t"
+        "s_load_dword %3, %10, 0xc0\n\t"
+        "s_load_dword %4, %10, 0x100\n\t"
+        "s_load_dword %5, %10, 0x140\n\t"
+        "s_load_dword %6, %10, 0x180\n\t"
+        "s_load_dword %7, %10, 0x200\n\t"
+        "s_load_dword %8, %10, 0x240\n\t"
+        "s_load_dword %9, %10, 0x280\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=s"(t0), "=s"(t1), "=s"(t2), "=s"(t3), "=s"(t4), "=s"(t5), "=s"(t6), "=s"(t7), "=s"(t8), "=s"(t9)
+        : "s"(__builtin_amdgcn_kernarg_segment_ptr())
+        : "memory");
+    (void)t0; (void)t1; (void)t2; (void)t3; (void)t4; (void)t5; (void)t6; (void)t7; (void)t8; (void)t9;
+}
+
 // c = f32(softmax scale (kernarg 0x050) x log2 e) split into 2^e m (the host checked that it is a positive normal)
 __device__ inline void set_qk_scale(Prm& p, bool on) {
     p.qk_scaled = on ? 1u : 0u;
@@ -163,6 +188,7 @@ __device__ inline void set_qk_scale(Prm& p, bool on) {
 // qk_e = 0 as constants (their code carries nothing of the extension).
 template <bool SC = false, bool KVS = false>
 __device__ inline Prm prm_from_kernarg() {
+    kernarg_lines_touch();
     Prm p;
     p.q = (const uint8_t*)KA_FIELD(uint64_t, ptr_q); p.k = (const uint8_t*)KA_FIELD(uint64_t, ptr_k);
     p.v = (const uint8_t*)KA_FIELD(uint64_t, ptr_v);
