@@ -242,6 +242,16 @@ def main():
                      "frac": round(kern_tflops / PEAK_MXFP8_TFLOPS, 4), "traffic": traffic,
                      "kernel": kern_name, "kernel_ms": round(kern_ms, 5)},
     }
+    if used[0] == "kvsplit":
+        # the KV split is HBM-bound (about 226 FLOP per byte at config 5, below the ridge of 5.0e15 / 8e12): its
+        # split kernel reads Q, K, V and their scales once and writes the fp16 partial rows and LSE words
+        rows = B * S * H
+        split_bytes = rows * (128 + 4) + 2 * B * SK * HK * 128 + B * SK * HK * 4 + used[1] * rows * (256 + 4)
+        gbs = split_bytes / (kern_ms * 1e-3) / 1e9
+        line["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "algorithmic_bytes": split_bytes,
+                            "kernel": kern_name, "kernel_ms": round(kern_ms, 5),
+                            "mfma_tflops": round(kern_tflops, 2), "mfma_frac": round(kern_tflops / PEAK_MXFP8_TFLOPS, 4)}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(B, H, HK, S, SK, causal)
     else:
