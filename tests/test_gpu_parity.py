@@ -327,7 +327,9 @@ def test_parity_vs128_split_tiles(gpu, case):
     inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
     out, used, _ = gpu_util.run(inp, gpu, path=force or "auto")
     assert used[0] == "vs128"
-    rows = oracle.first_and_last(S, 128)   # the first and the last q tile of every (b, h)
+    # every row where the emulation is cheap (every q tile and its XCD-remapped block), else the first and the last q
+    # tile of every (b, h)
+    rows = S if B * H * S * SK <= 10_000_000 else oracle.first_and_last(S, 128)
     emu, ref_stats = _emulated_bar(inp, 0, rows=rows, path="vs128")
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
@@ -336,9 +338,9 @@ def test_parity_vs128_split_tiles(gpu, case):
     assert stats["bad"] <= ref_stats["bad"]
     assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
     assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
-    # no element-wise maximum under the causal mask, as in test_parity_causal: in the first rows a few keys carry the
-    # whole weight, so one fp8 rounding of P that the MFMA's inexact sum moves shifts an output by a few % of |V|
-    # under the causal mask a looser element-wise bound (observed up to 0.094 over the causal cases)
+    # under the causal mask a looser element-wise bound, as in test_parity_causal: in the first rows a few keys carry
+    # the whole weight, so one fp8 rounding of P that the MFMA's inexact sum moves shifts an output by a few % of |V|
+    # (observed up to 0.094 over the causal cases)
     assert cmp["max_abs"] <= (0.25 if causal else 0.05), cmp
     if not causal:
         # the direct vs128 launcher keeps the 256-row kernel its grid names (the single-stream order), correct here too
