@@ -1276,8 +1276,15 @@ template <bool LUT, bool VS, bool SC>
 __device__ __forceinline__ void attend_single_wave(const Prm& p, uint32_t lds, uint32_t qtile, uint32_t head, uint32_t bidx) {
     constexpr int NT = 256;
     const Recipe rc = recipe(LUT);
+    const uint32_t tblk = (bidx * p.H + head) * ((p.S + 127u) / 128u) + qtile;
+    (void)tblk;
+    FMHA_MARK(p, tblk, 0);
+#ifdef FMHA_TRACE
+    if (p.trace && (threadIdx.x & 63u) == 0u) p.trace[((size_t)tblk * 8u + (threadIdx.x >> 6)) * 8u + 7u] = p.t_entry;
+#endif
     Wave<NT> w;
     w.init(p, lds, qtile, head, bidx, p.SK, wave_id());
+    FMHA_MARK(p, tblk, 1);
     const uint32_t kvh = head / p.gqa;
     const bool causal = (p.flags & 1u) != 0;
     uint32_t key_end = p.SK;
@@ -1289,8 +1296,6 @@ __device__ __forceinline__ void attend_single_wave(const Prm& p, uint32_t lds, u
     if (VS) st.init_vs(p.vs32 + (size_t)bidx * p.vs_b + kvh * kD, p.vs_row);
     auto key_of = [](uint32_t t) { return t * kTile; };
     auto slot_of = [](uint32_t t) { return t & 3u; };
-    const uint32_t tblk = (bidx * p.H + head) * ((p.S + 127u) / 128u) + qtile;
-    (void)tblk;
     FMHA_LDECL;
     if (ntiles > 0) {
         st.init_dma();
@@ -1306,7 +1311,9 @@ __device__ __forceinline__ void attend_single_wave(const Prm& p, uint32_t lds, u
         w.commit_q();
         // VMEM operations per tile: the K and V copies, the K-scale copy and (extension) the V-scale copy
         constexpr int kOps = 2 * Stager<NT>::kN + 1 + (VS ? 1 : 0);
+        FMHA_MARK(p, tblk, 2);
         block_barrier_keep_dma<0, kOps>();   // tiles 0 and 1 have landed; tile 2's copies stay in flight
+        FMHA_MARK(p, tblk, 3);
         v16f sa[4], sb[4];
         {
             w.template qk_all<0, 4, true>(0, sa);
@@ -1361,8 +1368,10 @@ __device__ __forceinline__ void attend_single_wave(const Prm& p, uint32_t lds, u
         last(sa);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no copy into LDS outlives the loop
     }
+    FMHA_MARK(p, tblk, 4);
     FMHA_LFLUSH(p, tblk);
     epilogue<false>(p, w, head, bidx, 0, rc, true);
+    FMHA_MARK(p, tblk, 5);
 }
 
 // Workgroup -> (q tile, head, z): consecutive tiles of one (batch, head) land on one XCD, so each XCD's L2 holds the K/V

@@ -30,7 +30,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_MXFP8_TFLOPS = 5000.0      # MI355X dense MXFP8 MFMA peak, published figure (5.0 PFLOP/s)
 PEAK_HBM_GBS = 8000.0           # MI355X HBM3E
-REF_PUBLISHED_TFLOPS = 1811.8   # reference, B4H8S2048 vs128 (BASELINE.md, docs/perf-matrix.md:41)
+REF_PUBLISHED_TFLOPS = 1811.8   # reference, B4H8S2048 vs128 (docs/perf-matrix.md:41)
 CLOCK_WARMUP_MS = 400.0         # wall time of untimed steps before any timing (the clock's ramp)
 REF_LAUNCHES, REF_REPS = 100, 5 # the reference's timing method (docs/perf-matrix.md:11)
 

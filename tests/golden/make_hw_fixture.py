@@ -4,7 +4,7 @@ recording what the hardware conversion and MFMA instructions return on fixed inp
 these instructions against it.
 
     python tests/golden/make_hw_fixture.py --build
-    python tests/golden/make_hw_fixture.py --run gpurun_out/hw_probe.npz     (on the GPU box)
+    python tests/golden/make_hw_fixture.py --run /tmp/hw_probe.npz           (on a machine with a gfx950 GPU)
 """
 import argparse
 import ctypes
