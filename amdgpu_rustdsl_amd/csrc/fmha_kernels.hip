@@ -249,11 +249,13 @@ __device__ inline uint32_t lane_addr(uint32_t uniform_base, uint32_t lane_off) {
 __device__ inline v4i lds_read16(uint32_t off) { return *(const LDS_AS v4i*)(uintptr_t)off; }
 __device__ inline uint32_t lds_read4(uint32_t off) { return *(const LDS_AS uint32_t*)(uintptr_t)off; }
 
-// A 16-byte vector store with system coherence (sc0 sc1: written through the L2). Used for the KV split's partial
-// rows, which the combine reads in the next launch from every XCD: written through, they leave no dirty lines for the
-// kernel-end write-back, and the split + combine pair runs 2-4 % faster on the 256-row shapes (measured on MI355X,
-// identical results). The s_nop is the wait state a VALU write of the data registers needs after a VMEM store of more
-// than 8 bytes; the compiler adds it after its own stores but not after inline asm.
+// A 16-byte vector store with system coherence (sc0 sc1: written through the L2), for every row the attention
+// kernels write: the output rows and the KV split's partial rows. Written through, they leave no dirty lines for the
+// kernel-end write-back of the L2, which otherwise runs after the last wave. Measured on MI355X, identical results:
+// cfg2 (B4H8S2048, 16 MiB of output) 33.6 -> 31.4 us, B1H8S8192 -2 %, the 128-row kernels -2 to -4 %, and the KV
+// split + combine pair 2-4 % on the 256-row shapes. (The combine's own output rows gained nothing measurable.) The
+// s_nop is the wait state a VALU write of the data registers needs after a VMEM store of more than 8 bytes; the
+// compiler adds it after its own stores but not after inline asm.
 __device__ inline void store16_system(void* ptr, v4i x) {
     asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 1" ::"v"(ptr), "v"(x) : "memory");
 }
@@ -1050,8 +1052,7 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
             const uint32_t r = 4u * k + (lane >> 4);
             const v4i x = lds_read16(sbase + r * kEpiRow + c16 * 16u);
             if (w.row0 + r < p.S) {
-                if (SPLIT) store16_system(obase + (size_t)r * ostride + c16 * 16u, x);
-                else *(v4i*)(obase + (size_t)r * ostride + c16 * 16u) = x;
+                store16_system(obase + (size_t)r * ostride + c16 * 16u, x);
             }
         }
     }
