@@ -20,6 +20,11 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// An 8-byte vector store written through the L2 (sc0 sc1), so that no dirty lines are left for the kernel-end write-back.
+__device__ inline void store8_system(void* ptr, u32x2 x) {
+    asm volatile("global_store_dwordx2 %0, %1, off sc0 sc1\n\ts_nop 1" ::"v"(ptr), "v"(x) : "memory");
+}
+
 __device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
@@ -126,7 +131,7 @@ extern "C" __global__ void __launch_bounds__(256) fmha_mxfp8_quant_rows(QuantRow
         // the row's four block bytes sit in lanes c = 0, 4, 8, 12 of its 16-lane group
         const uint32_t e1 = __shfl(e, base + 4, 64), e2 = __shfl(e, base + 8, 64), e3 = __shfl(e, base + 12, 64);
         if (row < a.rows) {
-            *reinterpret_cast<u32x2*>(a.q + row * 128u + c * 8u) = out;
+            store8_system(a.q + row * 128u + c * 8u, out);
             if (c == 0) *reinterpret_cast<uint32_t*>(a.scale + row * 4u) = e | (e1 << 8) | (e2 << 16) | (e3 << 24);
         }
     }
@@ -217,7 +222,7 @@ extern "C" __global__ void __launch_bounds__(256) fmha_mxfp8_quant_tensor(QuantT
             out[0] = pack4_e4m3(y[0], y[1], y[2], y[3]);
             out[1] = pack4_e4m3(y[4], y[5], y[6], y[7]);
             const uint64_t c = i + u * stride;
-            if (c < nchunk) *reinterpret_cast<u32x2*>(a.q + c * 8u) = out;
+            if (c < nchunk) store8_system(a.q + c * 8u, out);
         }
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) a.descale[0] = d;
