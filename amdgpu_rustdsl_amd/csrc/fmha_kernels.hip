@@ -260,6 +260,11 @@ __device__ inline void store16_system(void* ptr, v4i x) {
     asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 1" ::"v"(ptr), "v"(x) : "memory");
 }
 
+// The same for one word (the LSE outputs).
+__device__ inline void store4_system(void* ptr, float x) {
+    asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(ptr), "v"(x) : "memory");
+}
+
 __device__ inline v2i lds_read_tr8(uint32_t off) { return __builtin_amdgcn_ds_read_tr8_b64_v2i32((LDS_AS v2i*)(uintptr_t)off); }
 
 typedef float v8f __attribute__((ext_vector_type(8)));
@@ -1063,14 +1068,14 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
             const float hl = h2f(w.bw) + h2f(w.bw >> 16);
             const float lse2 = l > 0.0f ? __builtin_amdgcn_logf(l) - hl * 2048.0f + 127.0f + __builtin_amdgcn_logf(rc.conv) - rc.exp2_bias_log2
                                         : -INFINITY;
-            p.lse_out[((size_t)bidx * p.H + head) * p.S + row] = lse2 * 0.69314718055994531f;
+            store4_system(p.lse_out + ((size_t)bidx * p.H + head) * p.S + row, lse2 * 0.69314718055994531f);
         }
     } else {
         const float l_total = l * 0.0625f;
         const float hl = h2f(w.bw) + h2f(w.bw >> 16);
         const size_t prow = (size_t)split * p.rows_total + ((size_t)bidx * p.S + row) * p.H + head;
         // an empty range (l = 0) gets -1e30: the combine gives it weight 0
-        p.lse[prow] = l > 0.0f ? __builtin_amdgcn_logf(l_total) + (hl * 2048.0f) * -1.0f : -1.0e30f;
+        store4_system(p.lse + prow, l > 0.0f ? __builtin_amdgcn_logf(l_total) + (hl * 2048.0f) * -1.0f : -1.0e30f);
     }
 }
 
