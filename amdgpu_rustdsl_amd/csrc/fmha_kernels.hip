@@ -249,12 +249,12 @@ __device__ inline uint32_t lane_addr(uint32_t uniform_base, uint32_t lane_off) {
 __device__ inline v4i lds_read16(uint32_t off) { return *(const LDS_AS v4i*)(uintptr_t)off; }
 __device__ inline uint32_t lds_read4(uint32_t off) { return *(const LDS_AS uint32_t*)(uintptr_t)off; }
 
-// A 16-byte vector store with system coherence (sc0 sc1: written through the L2), for every row the attention
-// kernels write: the output rows and the KV split's partial rows. Written through, they leave no dirty lines for the
-// kernel-end write-back of the L2, which otherwise runs after the last wave. Measured on MI355X, identical results:
-// cfg2 (B4H8S2048, 16 MiB of output) 33.6 -> 31.4 us, B1H8S8192 -2 %, the 128-row kernels -2 to -4 %, and the KV
-// split + combine pair 2-4 % on the 256-row shapes. (The combine's own output rows gained nothing measurable.) The
-// s_nop is the wait state a VALU write of the data registers needs after a VMEM store of more than 8 bytes; the
+// A 16-byte vector store with system coherence (sc0 sc1: written through the L2), for every row the attention and
+// combine kernels write: the output rows and the KV split's partial rows. Written through, they leave no dirty lines
+// for the kernel-end write-back of the L2, which otherwise runs after the last wave. Measured on MI355X, identical
+// results: cfg2 (B4H8S2048, 16 MiB of output) 33.6 -> 31.4 us, B1H8S8192 -2 %, the 128-row kernels -2 to -4 %, the KV
+// split + combine pair 2-4 % on the 256-row shapes, and the combine's own rows -1.3 % more at B1H8S4096 (2 splits).
+// The s_nop is the wait state a VALU write of the data registers needs after a VMEM store of more than 8 bytes; the
 // compiler adds it after its own stores but not after inline asm.
 __device__ inline void store16_system(void* ptr, v4i x) {
     asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 1" ::"v"(ptr), "v"(x) : "memory");
@@ -1593,7 +1593,7 @@ extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvspli
     merge_init(st);
     if (split_field & FMHA_KVS_F32_PARTIALS) merge_splits<true>(lse, ohat, rows, 0u, splits, t, st);
     else merge_splits<false>(lse, ohat, rows, 0u, splits, t, st);
-    *(v4i*)((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u) = merge_finish(st);
+    store16_system((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u, merge_finish(st));
 }
 
 // Extension (no counterpart in the reference): the same merge for many splits, with the splits spread over the block's
@@ -1640,5 +1640,5 @@ extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvspli
         for (int i = 0; i < 8; ++i) o.acc[i] = part[q][2 + i][lane];
         merge_states(st, o);
     }
-    *(v4i*)((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u) = merge_finish(st);
+    store16_system((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u, merge_finish(st));
 }
