@@ -26,6 +26,11 @@ LIB = os.path.join(OUT, "libfmha_mxfp8.so")
 # the host pass warns that it does not know the feature, which is harmless.
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-command-line-argument"]
+# The attention kernels: MFMA accumulators and sources in the VGPR form. The 256-thread t128 kernel needs more than
+# 256 registers per wave; left to choose, the compiler placed the QK MFMAs' S accumulators in AGPRs and moved all 64
+# back to VGPRs for the softmax every tile (80 v_accvgpr moves per tile in the loop). In the VGPR form other values
+# take the AGPRs and the loop has none. The other kernels fit in 256 VGPRs and compile to the same code either way.
+FMHA_FLAGS = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def _run(cmd):
@@ -52,7 +57,7 @@ def code_object_calls(hsaco):
 def build(verbose=False):
     os.makedirs(OUT, exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
-    _run([hipcc, *HIP_FLAGS, "--genco", os.path.join(CSRC, "fmha_kernels.hip"), "-o", HSACO])
+    _run([hipcc, *HIP_FLAGS, *FMHA_FLAGS, "--genco", os.path.join(CSRC, "fmha_kernels.hip"), "-o", HSACO])
     _run([hipcc, *HIP_FLAGS, "--genco", os.path.join(CSRC, "quant_kernels.hip"), "-o", QHSACO])
     for co in (HSACO, QHSACO):
         calls = code_object_calls(co)
