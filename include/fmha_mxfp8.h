@@ -209,9 +209,11 @@ int fmha_mxfp8_select_path(int64_t B, int64_t H, int64_t S, int64_t SK, int* spl
 /* Extension (no counterpart in the reference): 1 if fmha_fwd_hd128_mxfp8_auto runs the full-sequence `path`
  * (FMHA_PATH_VS128 or FMHA_PATH_T128) on the split-tile kernel fmha_fwd_hd128_mxfp8_v3_t128_split_tiles (128-row
  * blocks of 512 threads, the two wave groups splitting each tile's keys and merging at the end), else 0. t128: at
- * least 4 key tiles. vs128: also a 256-row grid of at most 128 blocks, or `causal` (the 128-row grid's causal
- * q-tile pairing). The split-tile order rounds differently from the reference's single stream per row; the path and
- * its recipe are the reference's. */
+ * least 7 key tiles (4 with `causal`); below that the 256-thread fmha_fwd_hd128_mxfp8_v3_t128, which is faster there
+ * and keeps the reference's order. vs128: the same, and a 256-row grid of at most 128 blocks unless `causal` (the
+ * 128-row grid's causal q-tile pairing); such a half-chip grid below the threshold runs on the 256-thread t128
+ * kernel. The split-tile order rounds differently from the reference's single stream per row; the path and its
+ * recipe are the reference's. */
 int fmha_mxfp8_uses_split_tiles(int path, int64_t B, int64_t H, int64_t S, int64_t SK, int causal);
 
 /* Fill the kernarg fields derived from a packed [B,S,H,128] / [B,SK,HK,128]
@@ -242,7 +244,8 @@ int fmha_mxfp8_launch_t128(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, u
 /* Extension (no counterpart in the reference): the split-tile kernel fmha_fwd_hd128_mxfp8_v3_t128_split_tiles on
  * t128's grid (ceil(S/128), H, B) and kernarg layout, 512 threads; the two wave groups split each key tile and merge
  * at the end (the order fmha_mxfp8_uses_split_tiles names). fmha_fwd_hd128_mxfp8_auto runs it for t128's shapes with
- * at least 4 key tiles and for vs128's shapes whose 256-row grid has at most 128 blocks. */
+ * at least 7 key tiles (4 with the causal mask) and for vs128's shapes whose 256-row grid has at most 128 blocks
+ * (from the same key-tile counts). */
 int fmha_mxfp8_launch_t128_split_tiles(const fmha_mxfp8_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream);
 int fmha_mxfp8_launch_kvsplit(const fmha_mxfp8_kvsplit_args* a, uint32_t gx, uint32_t gy, uint32_t gz, void* stream);
 int fmha_mxfp8_launch_combine(const fmha_mxfp8_combine_args* a, uint32_t gx, void* stream);

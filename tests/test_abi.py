@@ -232,26 +232,29 @@ def test_select_path_matches_oracle():
 
 
 def test_uses_split_tiles_rule():
-    """Which full-sequence launches of the one-call entry run on the split-tile kernel: t128 from 4 key tiles on;
-    vs128 when its 256-row grid holds at most 128 blocks, also from 4 key tiles on (the LUT recipe keeps the
-    single-stream kernels); never the KV split's own kernel."""
-    assert lib.uses_split_tiles("t128", 1, 8, 512, 512)
+    """Which full-sequence launches of the one-call entry run on the split-tile kernel: t128 from 7 key tiles on (4
+    with the causal mask); vs128 from the same counts when its 256-row grid holds at most 128 blocks (always with
+    the causal mask); never the KV split's own kernel. Below the threshold the 256-thread t128 kernel runs."""
+    assert not lib.uses_split_tiles("t128", 1, 8, 512, 512)        # 4 key tiles: the single-wave kernel is faster
+    assert not lib.uses_split_tiles("t128", 1, 8, 512, 768)        # 6
+    assert lib.uses_split_tiles("t128", 1, 8, 512, 769)            # 7
+    assert lib.uses_split_tiles("t128", 1, 8, 512, 512, causal=True)
+    assert not lib.uses_split_tiles("t128", 1, 8, 100, 384, causal=True)   # 3 key tiles: LUT recipe
     assert not lib.uses_split_tiles("t128", 1, 1, 256, 256)        # 2 key tiles: LUT recipe
-    assert not lib.uses_split_tiles("t128", 1, 8, 100, 384)        # 3 key tiles
-    assert lib.uses_split_tiles("t128", 1, 8, 100, 385)            # 4 key tiles
     assert not lib.uses_split_tiles("vs128", 4, 8, 2048, 2048)     # 256 blocks: the whole chip already
     assert lib.uses_split_tiles("vs128", 2, 8, 2048, 2048)         # 128 blocks
     assert lib.uses_split_tiles("vs128", 4, 8, 1024, 1024)
-    assert lib.uses_split_tiles("vs128", 8, 8, 512, 512)
-    assert not lib.uses_split_tiles("vs128", 8, 8, 512, 384)       # LUT recipe
+    assert not lib.uses_split_tiles("vs128", 8, 8, 512, 512)       # 4 key tiles: on the 256-thread kernel
+    assert lib.uses_split_tiles("vs128", 8, 8, 512, 1024)
     assert not lib.uses_split_tiles("vs128", 2, 8, 2100, 1000)     # 9 x 8 x 2 = 144 blocks
     assert not lib.uses_split_tiles("vs128", 1, 8, 8192, 8192)
     assert not lib.uses_split_tiles("kvsplit", 1, 8, 2048, 2048)
-    for B, H, S, SK in ((1, 8, 2048, 2048), (2, 8, 2048, 2048), (4, 8, 512, 512), (3, 5, 777, 1500), (1, 1, 1, 1)):
+    for B, H, S, SK in ((1, 8, 2048, 2048), (2, 8, 2048, 2048), (4, 8, 512, 512), (3, 5, 777, 1500), (1, 1, 1, 1),
+                        (1, 8, 1024, 896)):
         path = lib.select_path(B, H, S, SK)[0]
         blocks256 = (S + 255) // 256 * H * B
         ntiles = (SK + 127) // 128
-        want = path in ("t128", "vs128") and ntiles >= 4 and (path == "t128" or blocks256 <= 128)
+        want = path in ("t128", "vs128") and ntiles >= 7 and (path == "t128" or blocks256 <= 128)
         assert lib.uses_split_tiles(path, B, H, S, SK) == want, (B, H, S, SK)
 
 

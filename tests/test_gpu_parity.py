@@ -269,7 +269,7 @@ def test_parity_qk_scale(gpu, case):
 # direct launcher fmha_mxfp8_launch_t128_split_tiles.
 T128_ST_CASES = [
     ("B1H8S1024", 1, 8, 8, 1024, 1024, False),
-    ("B2H8S512_gqa4", 2, 8, 2, 512, 512, False),
+    ("B2H8S512_SK1024_gqa4", 2, 8, 2, 512, 1024, False),
     ("B1H8S1000_SK1337", 1, 8, 8, 1000, 1337, False),
     ("B1H4S700_SK700_causal", 1, 4, 4, 700, 700, True),
     ("B1H2S100_SK2000", 1, 2, 2, 100, 2000, False),
@@ -311,7 +311,7 @@ def test_parity_t128_split_tiles(gpu, case):
 # (t128's 128-row grid, 512 threads); (name, B, H, HK, S, SK, causal, path forced or None)
 VS128_ST_CASES = [
     ("B2H8S2048", 2, 8, 8, 2048, 2048, False, None),
-    ("B8H8S512", 8, 8, 8, 512, 512, False, None),
+    ("B8H8S512_SK1024", 8, 8, 8, 512, 1024, False, None),
     ("B4H8HK2_S1024_gqa4", 4, 8, 2, 1024, 1024, False, None),
     ("B2H8S2048_SK1337", 2, 8, 8, 2048, 1337, False, None),
     ("B1H4S700_SK900_forced", 1, 4, 4, 700, 900, False, "vs128"),
@@ -472,3 +472,37 @@ def test_parity_kv_fill(gpu, case):
         assert st["mean_err"] <= 1.10 * ref_stats["mean_err"]
     assert cmp["mean_abs"] <= 0.6 * ref_stats["mean_err"], cmp
     assert cmp["max_abs"] <= 0.05, cmp
+
+
+# The 128-row grids below the split-tile threshold (4 to 6 key tiles, no causal mask): the one-call entry runs them on
+# the 256-thread t128 kernel, the reference's order. t128's shapes must give the direct t128 launcher's bits, and
+# vs128's half-chip shapes the direct vs128 launcher's (the 256-row kernel takes every tile whole too); both meet the
+# bar against the emulation of the reference's order.
+SINGLE_WAVE_CASES = [
+    ("t128_B1H8S512", 1, 8, 8, 512, 512, "t128"),
+    ("t128_B2H8HK2_S700_SK700", 2, 8, 2, 700, 700, "t128"),
+    ("t128_B1H4S300_SK600", 1, 4, 4, 300, 600, "t128"),
+    ("vs128_B8H8S512", 8, 8, 8, 512, 512, "vs128"),
+    ("vs128_B2H8S2048_SK768", 2, 8, 8, 2048, 768, "vs128"),
+]
+
+
+@pytest.mark.parametrize("case", SINGLE_WAVE_CASES, ids=[c[0] for c in SINGLE_WAVE_CASES])
+def test_parity_128row_single_wave(gpu, case):
+    name, B, H, HK, S, SK, path = case
+    print(f"[case] single wave {name}", flush=True)
+    assert not lib.uses_split_tiles(path, B, H, S, SK)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK)
+    out, used, _ = gpu_util.run(inp, gpu, path=path)
+    assert used == (path, 0)
+    rows = S if B * H * S * SK <= 10_000_000 else oracle.first_and_last(S, 128)
+    emu, ref_stats = _emulated_bar(inp, 0, rows=rows, path=path)
+    stats = oracle.check_fp64(inp, out, rows=rows)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
+    print(f"[case] single wave {name} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
+    assert not np.isnan(oracle.bf16_to_f32(out)).any()
+    assert stats["bad"] <= ref_stats["bad"]
+    assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
+    assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
+    assert cmp["max_abs"] <= 0.05, cmp
+    np.testing.assert_array_equal(gpu_util.run_direct(inp, gpu, path), out)
