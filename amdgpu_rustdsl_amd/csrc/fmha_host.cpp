@@ -96,33 +96,33 @@ const char* const kKernelNames[10] = {
 enum { K_VS128 = 0, K_T128 = 1, K_KVSPLIT = 2, K_COMBINE = 3, K_VS128_SC = 4, K_T128_SC = 5, K_KVSPLIT_SC = 6, K_T128ST = 7,
        K_T128ST_SC = 8, K_COMBINE_WIDE = 9 };
 
-// The 128-row grids (t128's shapes, and vs128's half-chip ones below) run on the split-tile kernel (512 threads) from
-// 7 key tiles on, and on the one-wave-per-SIMD kernel (256 threads, the reference's order) below that: with 4 to 6
-// key tiles the single-wave kernel is faster (measured on MI355X, us: B1H8S512 9.11 against 9.92, B1H8S1024 SK768
-// 11.52 against 11.73, B4H8S512 9.45 against 10.28; at SK1024 13.78 against 13.16), and with fewer than 4 (the LUT
-// recipe, state.rs:75-77) it keeps the reference's order. Causal shapes take the split-tile kernel from 4 key tiles
-// on (it is ahead there: B1H8S1024 causal 13.56 against 14.45), where the causal q-tile pairing is available.
-bool use_split_tiles(int64_t SK, bool causal) { return (SK + 127) / 128 >= (causal ? 4 : 7); }
-int t128_kernel(uint32_t SK, bool causal, bool scaled, uint32_t* block) {
-    const bool st = use_split_tiles(SK, causal);
-    *block = st ? 512u : 256u;
-    return st ? (scaled ? K_T128ST_SC : K_T128ST) : (scaled ? K_T128_SC : K_T128);
+// The 128-row grids (t128's shapes, and vs128's half-chip and causal ones below) run on the split-tile kernel (512
+// threads) from 7 key tiles on, and on the one-wave-per-SIMD kernel (256 threads, the reference's order) below that:
+// with 4 to 6 key tiles the single-wave kernel is faster (measured on MI355X, us: B1H8S512 9.11 against 9.92,
+// B1H8S1024 SK768 11.52 against 11.73, B4H8S512 9.45 against 10.28, B8H8S512 9.78 against 10.75; at SK1024 13.78
+// against 13.16), and with fewer than 4 (the LUT recipe, state.rs:75-77) it keeps the reference's order. Causal
+// shapes take the split-tile kernel from 4 key tiles on (unpaired it is ahead: B1H8S1024 causal 13.56 against 14.45)
+// except on grids the causal q-tile pairing halves (more 128-row blocks than CUs) with at most 8 key tiles, where the
+// single-wave kernel runs each pair faster (B16H8S512 15.13 against 17.07, B8H8S768 16.94 against 18.34, B8H8S1024
+// 19.45 against 20.13; at 16 tiles, B4H8S2048, 28.37 against 26.63). The choice does not depend on the causal_pair
+// field, so a forced pairing gives the same kernel, and so the same bits, as the automatic one.
+int cu_count();
+bool use_split_tiles(int64_t B, int64_t H, int64_t S, int64_t SK, bool causal) {
+    const int64_t tiles = (SK + 127) / 128;
+    if (!causal) return tiles >= 7;
+    if (tiles < 4) return false;
+    return !(tiles <= 8 && (S + 127) / 128 * H * B > (int64_t)cu_count());
 }
 
 // The one-call entry also runs the vs128 path on the 128-row grid when its 256-row grid holds at most 128 blocks (half
-// of the 256 CUs or fewer): there the same shape fills twice the CUs. The kernel is chosen as for t128 (above). The
-// direct vs128 launcher keeps the 256-row kernel its grid names. Causal (extension): always from 4 key tiles on, so
-// that the 128-row grid's causal q-tile pairing is available past one wave of blocks.
-bool vs128_split_tiles(int64_t B, int64_t H, int64_t S, int64_t SK, bool causal) {
-    return (causal || (S + 255) / 256 * H * B <= 128) && use_split_tiles(SK, causal);
-}
-
-// Below the split-tile threshold such a half-chip vs128 grid runs on the 256-thread t128 kernel: the same order and
-// bits as the vs128 kernel (both take every tile whole), on twice the blocks. Measured with the LUT recipe at B4H8S1024
-// SK256, B2H8S2048 SK384 and B1H8S4096 SK128: 10.4 / 12.6 / 7.7 us against 11.9 / 14.3 / 9.5 (above 128 blocks of
-// 256 rows the vs128 kernel stays ahead: B8H8S2048 SK256 25.4 against 36.4 us).
-bool vs128_on_t128(int64_t B, int64_t H, int64_t S, int64_t SK, bool causal) {
-    return (S + 255) / 256 * H * B <= 128 && !use_split_tiles(SK, causal);
+// of the 256 CUs or fewer): there the same shape fills twice the CUs. Causal (extension): always from 4 key tiles on,
+// so that the 128-row grid's causal q-tile pairing is available past one wave of blocks. The kernel is chosen as for
+// t128 (above). Below the split-tile threshold the 256-thread t128 kernel gives the vs128 kernel's order and bits
+// (both take every tile whole) on twice the blocks; measured with the LUT recipe at B4H8S1024 SK256, B2H8S2048 SK384
+// and B1H8S4096 SK128: 10.4 / 12.6 / 7.7 us against 11.9 / 14.3 / 9.5 (above 128 blocks of 256 rows the vs128 kernel
+// stays ahead: B8H8S2048 SK256 25.4 against 36.4 us). The direct vs128 launcher keeps the 256-row kernel its grid names.
+bool vs128_on_128row_grid(int64_t B, int64_t H, int64_t S, int64_t SK, bool causal) {
+    return (S + 255) / 256 * H * B <= 128 || (causal && (SK + 127) / 128 >= 4);
 }
 
 fmha_internal::ModuleCache<10> g_fmha(fmha_mxfp8_hsaco_begin, fmha_mxfp8_hsaco_end, kKernelNames);
@@ -326,8 +326,9 @@ int fmha_mxfp8_validate_combine(const fmha_mxfp8_combine_args* a, const fmha_mxf
 }
 
 int fmha_mxfp8_uses_split_tiles(int path, int64_t B, int64_t H, int64_t S, int64_t SK, int causal) {
-    if (path == FMHA_PATH_T128) return use_split_tiles(SK, causal != 0) ? 1 : 0;
-    if (path == FMHA_PATH_VS128) return vs128_split_tiles(B, H, S, SK, causal != 0) ? 1 : 0;
+    if (path == FMHA_PATH_T128) return use_split_tiles(B, H, S, SK, causal != 0) ? 1 : 0;
+    if (path == FMHA_PATH_VS128)
+        return vs128_on_128row_grid(B, H, S, SK, causal != 0) && use_split_tiles(B, H, S, SK, causal != 0) ? 1 : 0;
     return 0;
 }
 
@@ -472,16 +473,14 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
         }
         uint32_t block = 512u, kgx = gx;
         int kern;
-        if (path == FMHA_PATH_T128) {
-            kern = t128_kernel((uint32_t)SK, p->causal != 0, scaled, &block);
-        } else if (vs128_split_tiles(B, H, S, SK, p->causal != 0)) {
-            kern = scaled ? K_T128ST_SC : K_T128ST;   // same kernarg layout, 128-row grid
-            kgx = (uint32_t)((S + 127) / 128);
-        } else if (vs128_on_t128(B, H, S, SK, p->causal != 0)) {
-            kern = t128_kernel((uint32_t)SK, p->causal != 0, scaled, &block);   // the 256-thread kernel: same kernargs, 128-row grid
-            kgx = (uint32_t)((S + 127) / 128);
-        } else {
+        if (path == FMHA_PATH_VS128 && !vs128_on_128row_grid(B, H, S, SK, p->causal != 0)) {
             kern = scaled ? K_VS128_SC : K_VS128;
+        } else {
+            // t128, or vs128 on the 128-row grid (same kernarg layout): the split-tile kernel or the 256-thread one
+            const bool st = use_split_tiles(B, H, S, SK, p->causal != 0);
+            kern = st ? (scaled ? K_T128ST_SC : K_T128ST) : (scaled ? K_T128_SC : K_T128);
+            block = st ? 512u : 256u;
+            kgx = (uint32_t)((S + 127) / 128);
         }
         // the causal q-tile pairing when the grid would take more than one wave of blocks (the extension's flag; the
         // reference pairs its causal kernels' tiles always, grid.rs:94-111), or when the caller asks for it

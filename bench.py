@@ -404,9 +404,10 @@ def kernel_launcher(lib, q, k, v, qs, ks, vs, out, lse, used, B, H, HK, S, SK, c
     if path in ("vs128", "t128"):
         split_tiles = lib.uses_split_tiles(path, B, H, S, SK, causal)
         # the kernel the one-call entry runs: the split-tile kernel (t128's grid, 512 threads), the 256-thread t128
-        # kernel (vs128's half-chip grids below the split-tile threshold) or the path's own
-        half_chip = math.ceil(S / 256) * H * B <= 128
-        on_t128 = path == "t128" or split_tiles or half_chip
+        # kernel (128-row grids below the split-tile threshold) or the path's own; vs128 takes the 128-row grid when
+        # its 256-row grid is at most half the chip, and under the causal mask from 4 key tiles on
+        row128 = math.ceil(S / 256) * H * B <= 128 or (causal and math.ceil(SK / 128) >= 4)
+        on_t128 = path == "t128" or split_tiles or row128
         grid = (math.ceil(S / (128 if on_t128 else 256)), H, B)
         rc, msg = lib.validate("t128" if on_t128 else "vs128", a, sz, grid, HK=HK)
         assert rc == 0, msg

@@ -241,6 +241,11 @@ def test_uses_split_tiles_rule():
     assert lib.uses_split_tiles("t128", 1, 8, 512, 512, causal=True)
     assert not lib.uses_split_tiles("t128", 1, 8, 100, 384, causal=True)   # 3 key tiles: LUT recipe
     assert not lib.uses_split_tiles("t128", 1, 1, 256, 256)        # 2 key tiles: LUT recipe
+    # causal grids that the pairing halves (more 128-row blocks than CUs) with at most 8 key tiles: single-wave
+    assert not lib.uses_split_tiles("t128", 16, 8, 512, 512, causal=True)
+    assert not lib.uses_split_tiles("vs128", 8, 8, 1024, 1024, causal=True)
+    assert lib.uses_split_tiles("vs128", 8, 8, 1152, 1152, causal=True)      # 9 key tiles
+    assert lib.uses_split_tiles("vs128", 4, 8, 1024, 1024, causal=True)      # 256 blocks: not paired
     assert not lib.uses_split_tiles("vs128", 4, 8, 2048, 2048)     # 256 blocks: the whole chip already
     assert lib.uses_split_tiles("vs128", 2, 8, 2048, 2048)         # 128 blocks
     assert lib.uses_split_tiles("vs128", 4, 8, 1024, 1024)
