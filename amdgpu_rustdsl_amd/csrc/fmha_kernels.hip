@@ -66,12 +66,16 @@ constexpr int kLdsKsDummy = kLdsKs + kSlots * kKsSlot;   // 1 KiB sink for the K
 constexpr int kVsSlot = 512;
 constexpr int kLdsVs = kLdsKsDummy + 1024;
 constexpr int kLdsVsSink = kLdsVs + kSlots * kVsSlot;
-constexpr int kLdsBytes = kLdsVsSink + 2048;
 // epilogue staging of the output rows (after the loop, over the dead ring): 32 rows of 272 B per wave, above the
 // 68 KiB the split-tile merge uses
 constexpr int kLdsEpi = 68 * 1024;
 constexpr int kEpiRow = 272;
-static_assert(kLdsEpi + 8 * 32 * kEpiRow <= kLdsBytes, "epilogue staging fits");
+// the ping-pong kernels' group B stages its rows apart from the ring while group A still reads it: 16 rows of 272 B
+// per wave slot at a time, 4 slots
+constexpr int kLdsTail = kLdsVsSink + 2048;
+constexpr int kLdsBytes = kLdsTail + 4 * 16 * kEpiRow;
+static_assert(kLdsEpi + 8 * 32 * kEpiRow <= kLdsTail, "epilogue staging fits");
+static_assert(kLdsBytes <= 160 * 1024, "LDS of one workgroup");
 
 struct Prm {
     const uint8_t* q;
@@ -978,8 +982,12 @@ __device__ __forceinline__ v4i merge_finish(const MergeState& st) {
 // split * rows_total + (b S + row) H + h. A row with no visible key (causal, S > SK) writes zeros.
 // The 16-bit rows go through LDS: each lane holds 4-dim pieces of one row (the MFMA C layout), so direct stores would
 // touch 32 rows (32 cache lines) per instruction; staged as [32 rows][256 B] per wave, 16 lanes write one row's 256 B
-// with 16-byte stores. `sync`: the ring may still be read by other waves (a block barrier first).
-template <bool SPLIT, int NT>
+// with 16-byte stores. `sync`: the ring may still be read by other waves (a block barrier first). TAIL (the ping-pong
+// kernels' group B, which ends its loop one MFMA phase before group A): the rows go through the wave's own slot past
+// the ring in two rounds of 16 rows, without waiting for A, and B's block barrier, which pairs with the one A takes
+// before staging over the ring, comes after B's stores are issued. (The 256-thread kernel's waves end together:
+// there the two rounds cost more than the barrier saves.)
+template <bool SPLIT, int NT, bool TAIL = false>
 __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32_t head, uint32_t bidx, uint32_t split, const Recipe& rc,
                                          bool sync) {
     // lane-derived values recomputed here from an opaque lane id: kept from the prologue they would be live (and
@@ -1025,40 +1033,71 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
                 }
         }
     } else {
-        if (sync) block_barrier();
-        const uint32_t sbase = w.lds + kLdsEpi + wave_id() * 32u * kEpiRow;
+        if (sync && !TAIL) block_barrier();
         const float fin16 = fin * 0.0625f;   // (x / 16) fin == x (fin / 16) exactly: 1/16 is a power of two
+        // the row's 16-bit words: wd[dc][a][c] holds dims 32 dc + 8 a + dbase + 2 c and + 1
+        uint32_t wd[4][4][2];
 #pragma unroll
         for (int dc = 0; dc < 4; ++dc)
 #pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                uint32_t wd[2];
+            for (int a = 0; a < 4; ++a)
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
                     const float x0 = w.o[dc][4 * a + 2 * c], x1 = w.o[dc][4 * a + 2 * c + 1];
                     if (!SPLIT) {
                         const v2bf b = {(__bf16)(x0 * fin), (__bf16)(x1 * fin)};
-                        wd[c] = __builtin_bit_cast(uint32_t, b);
+                        wd[dc][a][c] = __builtin_bit_cast(uint32_t, b);
                     } else {
                         // the f32 products are rounded, then converted to f16 (RNE): the empty asm keeps the compiler
                         // from fusing product and conversion into one rounding (v_fma_mix), which differs in
                         // double-rounding cases; v_cvt_pk_f16_f32 converts the pair
                         float y0 = x0 * fin16, y1 = x1 * fin16;
                         asm volatile("" : "+v"(y0), "+v"(y1));
-                        wd[c] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){y0, y1}, v2h));
+                        wd[dc][a][c] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){y0, y1}, v2h));
                     }
                 }
-                *(LDS_AS v2i*)(uintptr_t)(sbase + n * kEpiRow + (32 * dc + 8 * a + dbase) * 2) = (v2i){(int)wd[0], (int)wd[1]};
-            }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave reads back only its own rows
         const uint32_t c16 = lane & 15u;
+        if (!TAIL) {
+            const uint32_t sbase = w.lds + kLdsEpi + wave_id() * 32u * kEpiRow;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t r = 4u * k + (lane >> 4);
-            const v4i x = lds_read16(sbase + r * kEpiRow + c16 * 16u);
-            if (w.row0 + r < p.S) {
-                store16_system(obase + (size_t)r * ostride + c16 * 16u, x);
+            for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+                    *(LDS_AS v2i*)(uintptr_t)(sbase + n * kEpiRow + (32 * dc + 8 * a + dbase) * 2) = (v2i){(int)wd[dc][a][0], (int)wd[dc][a][1]};
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave reads back only its own rows
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t r = 4u * k + (lane >> 4);
+                const v4i x = lds_read16(sbase + r * kEpiRow + c16 * 16u);
+                if (w.row0 + r < p.S) {
+                    store16_system(obase + (size_t)r * ostride + c16 * 16u, x);
+                }
             }
+        } else {
+            // rows 16 h .. 16 h + 15 per round (the lanes of those rows write, every lane reads back and stores)
+            const uint32_t sbase = w.lds + kLdsTail + (wave_id() & 3u) * 16u * kEpiRow;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if ((n >> 4) == (uint32_t)h) {
+#pragma unroll
+                    for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+                        for (int a = 0; a < 4; ++a)
+                            *(LDS_AS v2i*)(uintptr_t)(sbase + (n & 15u) * kEpiRow + (32 * dc + 8 * a + dbase) * 2) =
+                                (v2i){(int)wd[dc][a][0], (int)wd[dc][a][1]};
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t r = 4u * k + (lane >> 4);
+                    const v4i x = lds_read16(sbase + r * kEpiRow + c16 * 16u);
+                    if (w.row0 + 16u * h + r < p.S) {
+                        store16_system(obase + (size_t)(16u * h + r) * ostride + c16 * 16u, x);
+                    }
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // round h's reads are back before h + 1 writes
+            }
+            if (sync) block_barrier();   // pairs with A's barrier before its staging
         }
     }
     if (row >= p.S || hh != 0) return;
@@ -1256,7 +1295,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     FMHA_LFLUSH(p, tblk);
     // HV: B's state is in A's now, and only A writes (B goes on to the end: the causal pairing's second pass follows
     // a block barrier)
-    if (!HV || merge_halves<GB>(w, lds)) epilogue<SPLIT>(p, w, head, bidx, split, rc, !HV);   // HV: the merge's barriers retired the ring
+    if (!HV || merge_halves<GB>(w, lds)) epilogue<SPLIT, NT, GB && !HV>(p, w, head, bidx, split, rc, !HV);   // HV: the merge's barriers retired the ring
     FMHA_MARK(p, tblk, 5);
 }
 
