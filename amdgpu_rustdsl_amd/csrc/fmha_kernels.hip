@@ -986,8 +986,9 @@ __device__ __forceinline__ v4i merge_finish(const MergeState& st) {
 // kernels' group B, which ends its loop one MFMA phase before group A): the rows go through the wave's own slot past
 // the ring in two rounds of 16 rows, without waiting for A, and B's block barrier, which pairs with the one A takes
 // before staging over the ring, comes after B's stores are issued. (The 256-thread kernel's waves end together:
-// there the two rounds cost more than the barrier saves.)
-template <bool SPLIT, int NT, bool TAIL = false>
+// there the two rounds cost more than the barrier saves.) DCH: the dims the wave writes: 0 all, 1 dims 0..63 (dc 0, 1),
+// 2 dims 64..127 (dc 2, 3; the LSE is left to the DCH 1 wave of the same rows).
+template <bool SPLIT, int NT, bool TAIL = false, int DCH = 0>
 __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32_t head, uint32_t bidx, uint32_t split, const Recipe& rc,
                                          bool sync) {
     // lane-derived values recomputed here from an opaque lane id: kept from the prologue they would be live (and
@@ -999,6 +1000,8 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
     const float l = row_sum(w.lacc, lane);
     const uint32_t dbase = 4u * hh;
     const bool f32 = SPLIT && p.f32_partials;
+    constexpr int kDc0 = DCH == 2 ? 2 : 0, kDc1 = DCH == 1 ? 2 : 4;   // the dc range written
+    static_assert(!(TAIL && DCH != 0), "the tail staging writes whole rows");
     // per-lane factor and 16-bit conversion of the row pieces
     float fin;
     if (!SPLIT) {
@@ -1023,7 +1026,7 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
         if (row < p.S) {
             uint8_t* orow = obase + (size_t)n * ostride;
 #pragma unroll
-            for (int dc = 0; dc < 4; ++dc)
+            for (int dc = kDc0; dc < kDc1; ++dc)
 #pragma unroll
                 for (int a = 0; a < 4; ++a) {
                     v4f x;
@@ -1038,7 +1041,7 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
         // the row's 16-bit words: wd[dc][a][c] holds dims 32 dc + 8 a + dbase + 2 c and + 1
         uint32_t wd[4][4][2];
 #pragma unroll
-        for (int dc = 0; dc < 4; ++dc)
+        for (int dc = kDc0; dc < kDc1; ++dc)
 #pragma unroll
             for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -1060,17 +1063,30 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
         if (!TAIL) {
             const uint32_t sbase = w.lds + kLdsEpi + wave_id() * 32u * kEpiRow;
 #pragma unroll
-            for (int dc = 0; dc < 4; ++dc)
+            for (int dc = kDc0; dc < kDc1; ++dc)
 #pragma unroll
                 for (int a = 0; a < 4; ++a)
                     *(LDS_AS v2i*)(uintptr_t)(sbase + n * kEpiRow + (32 * dc + 8 * a + dbase) * 2) = (v2i){(int)wd[dc][a][0], (int)wd[dc][a][1]};
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave reads back only its own rows
+            if (DCH == 0) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const uint32_t r = 4u * k + (lane >> 4);
-                const v4i x = lds_read16(sbase + r * kEpiRow + c16 * 16u);
-                if (w.row0 + r < p.S) {
-                    store16_system(obase + (size_t)r * ostride + c16 * 16u, x);
+                for (int k = 0; k < 8; ++k) {
+                    const uint32_t r = 4u * k + (lane >> 4);
+                    const v4i x = lds_read16(sbase + r * kEpiRow + c16 * 16u);
+                    if (w.row0 + r < p.S) {
+                        store16_system(obase + (size_t)r * ostride + c16 * 16u, x);
+                    }
+                }
+            } else {
+                // half rows: 8 lanes store one row's 128 B
+                const uint32_t c8 = (lane & 7u) + (DCH == 2 ? 8u : 0u);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t r = 8u * k + (lane >> 3);
+                    const v4i x = lds_read16(sbase + r * kEpiRow + c8 * 16u);
+                    if (w.row0 + r < p.S) {
+                        store16_system(obase + (size_t)r * ostride + c8 * 16u, x);
+                    }
                 }
             }
         } else {
@@ -1100,7 +1116,7 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
             if (sync) block_barrier();   // pairs with A's barrier before its staging
         }
     }
-    if (row >= p.S || hh != 0) return;
+    if (row >= p.S || hh != 0 || DCH == 2) return;
     if (!SPLIT) {
         if (p.lse_out) {
             // natural-log LSE of the scores (extension): P = 2^(S + 512 b - 127) / conv, l = sum P
@@ -1118,49 +1134,58 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
     }
 }
 
-// The two key halves of one row block (HV): group B's wave w + 4 writes its softmax state (the 64 O values of each
-// lane as 16 four-value groups, then the row sum and the bias word) to LDS, 16 bytes per lane and group, lane-contiguous,
-// over the dead K/V ring; A's wave w, holding the same rows, reads it and merges: with b the stream's bias (O and l
-// carry a factor 2^(512 b)), the smaller b is kept and the other stream is scaled by 2^(512 (b_min - b)) <= 1. An empty
-// stream (b = 64, O = l = 0) adds zeros. Returns whether the wave goes on to the epilogue (A) or is done (B). Every
-// wave of the block calls it (two block barriers).
+// The two key halves of one row block (HV): wave w of group A (waves 0-3) and wave w + 4 of group B hold the same 32
+// rows in the same lane layout, each with the softmax state of its half of every tile's keys. Each hands the other
+// the O values of the dims the other finishes: B gives A dims 0..63 (O groups dc 0, 1), A gives B dims 64..127
+// (dc 2, 3), as 8 four-value groups, 16 bytes per lane and group, lane-contiguous, over the dead K/V ring, with its
+// row sum and bias word. With b the stream's bias (O and l carry a factor 2^(512 b)), the smaller b is kept and the
+// other stream is scaled by 2^(512 (b_min - b)) <= 1; an empty stream (b = 64, O = l = 0) adds zeros. Both groups
+// evaluate the same expressions on the same operands (A's stream times sa, B's times sb, B's added by the fma), so
+// the merged row sum and bias word agree bit for bit and each group writes its half of every row. Every wave of the
+// block calls it (two block barriers).
 // (Whole v4 groups: stores of single elements extracted from the accumulators were merged by the compiler into
 // ds_write2st64 pairs that repeated one element.)
 template <bool GB, int NT>
-__device__ __forceinline__ bool merge_halves(Wave<NT>& w, uint32_t lds) {
-    constexpr uint32_t kGroups = 17u;   // 16 groups of O values, then (row sum, bias word, -, -)
+__device__ __forceinline__ void merge_halves(Wave<NT>& w, uint32_t lds) {
+    constexpr uint32_t kGroups = 17u;   // B -> A groups 0..7, A -> B groups 8..15, then (l_a, bw_a, l_b, bw_b)
+    constexpr int kGive = GB ? 0 : 2;   // the dc pair this group hands over
+    constexpr int kKeep = GB ? 2 : 0;   // the dc pair it finishes
     block_barrier();                    // every wave is done with the ring (its copies drained before)
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t base = lds + kLdsK + (wave_id() & 3u) * kGroups * 1024u + lane * 16u;
-    if (GB) {
+    const float l_own = row_sum(w.lacc, lane);
 #pragma unroll
-        for (int g = 0; g < 16; ++g) {
-            const v16f& od = w.o[g >> 2];
-            const v4f x = {od[4 * (g & 3)], od[4 * (g & 3) + 1], od[4 * (g & 3) + 2], od[4 * (g & 3) + 3]};
-            lds_write16(base + (uint32_t)g * 1024u, __builtin_bit_cast(v4i, x));
-        }
-        lds_write16(base + 16u * 1024u, (v4i){__builtin_bit_cast(int, row_sum(w.lacc, lane)), (int)w.bw, 0, 0});
+    for (int g = 0; g < 8; ++g) {
+        const v16f& od = w.o[kGive + (g >> 2)];
+        const v4f x = {od[4 * (g & 3)], od[4 * (g & 3) + 1], od[4 * (g & 3) + 2], od[4 * (g & 3) + 3]};
+        lds_write16(base + (uint32_t)(GB ? g : 8 + g) * 1024u, __builtin_bit_cast(v4i, x));
     }
+    *(LDS_AS v2i*)(uintptr_t)(base + 16u * 1024u + (GB ? 8u : 0u)) = (v2i){__builtin_bit_cast(int, l_own), (int)w.bw};
     block_barrier();
-    if (GB) return false;
-    const v4i st = lds_read16(base + 16u * 1024u);
-    const uint32_t bw_b = (uint32_t)st[1];
-    const float l_b = __builtin_bit_cast(float, st[0]);
-    const float b_a = bias_of(w.bw), b_b = bias_of(bw_b);
+    const v2i so = *(const LDS_AS v2i*)(uintptr_t)(base + 16u * 1024u + (GB ? 0u : 8u));
+    const float l_a = GB ? __builtin_bit_cast(float, so[0]) : l_own;
+    const float l_b = GB ? l_own : __builtin_bit_cast(float, so[0]);
+    const uint32_t bw_a = GB ? (uint32_t)so[1] : w.bw;
+    const uint32_t bw_b = GB ? w.bw : (uint32_t)so[1];
+    const float b_a = bias_of(bw_a), b_b = bias_of(bw_b);
     const bool keep_a = b_a <= b_b;
     const float sc = __builtin_amdgcn_exp2f(512.0f * (keep_a ? b_a - b_b : b_b - b_a));
     const float sa = keep_a ? 1.0f : sc, sb = keep_a ? sc : 1.0f;
 #pragma unroll
-    for (int g = 0; g < 16; ++g) {
-        const v4f ob = __builtin_bit_cast(v4f, lds_read16(base + (uint32_t)g * 1024u));
+    for (int g = 0; g < 8; ++g) {
+        const v4f ot = __builtin_bit_cast(v4f, lds_read16(base + (uint32_t)(GB ? 8 + g : g) * 1024u));
+        v16f& od = w.o[kKeep + (g >> 2)];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w.o[g >> 2][4 * (g & 3) + e] = __builtin_fmaf(ob[e], sb, w.o[g >> 2][4 * (g & 3) + e] * sa);
+        for (int e = 0; e < 4; ++e) {
+            const float oa = GB ? ot[e] : od[4 * (g & 3) + e];
+            const float ob = GB ? od[4 * (g & 3) + e] : ot[e];
+            od[4 * (g & 3) + e] = __builtin_fmaf(ob, sb, oa * sa);
+        }
     }
-    const float l = __builtin_fmaf(l_b, sb, row_sum(w.lacc, lane) * sa);
+    const float l = __builtin_fmaf(l_b, sb, l_a * sa);
     w.lacc[0] = l;
     w.lacc[1] = l;
-    w.bw = keep_a ? w.bw : bw_b;
-    return true;
+    w.bw = keep_a ? bw_a : bw_b;
 }
 
 // Two 4-wave groups one phase apart (waves 0-3: A, 4-7: B; the hardware places waves w and w + 4 on one SIMD).
@@ -1293,9 +1318,13 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     }
     FMHA_MARK(p, tblk, 4);
     FMHA_LFLUSH(p, tblk);
-    // HV: B's state is in A's now, and only A writes (B goes on to the end: the causal pairing's second pass follows
-    // a block barrier)
-    if (!HV || merge_halves<GB>(w, lds)) epilogue<SPLIT, NT, GB && !HV>(p, w, head, bidx, split, rc, !HV);   // HV: the merge's barriers retired the ring
+    if (!HV) {
+        epilogue<SPLIT, NT, GB>(p, w, head, bidx, split, rc, true);
+    } else {
+        // HV: each group finishes half of every row's dims (A 0..63, B 64..127); the merge's barriers retired the ring
+        merge_halves<GB>(w, lds);
+        epilogue<SPLIT, NT, false, GB ? 2 : 1>(p, w, head, bidx, split, rc, false);
+    }
     FMHA_MARK(p, tblk, 5);
 }
 
