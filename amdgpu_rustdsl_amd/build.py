@@ -54,6 +54,40 @@ def code_object_calls(hsaco):
     return [l.strip() for l in dis.splitlines() if "s_swappc_b64" in l or "s_call_b64" in l]
 
 
+# Instructions that read M0 implicitly (gfx950). The direct HBM -> LDS copies of the attention kernels set M0 in inline
+# assembly; a compiler-emitted reader would see their value.
+_M0_READERS = ("s_sendmsg", "ds_gws", "ds_append", "ds_consume", "ds_read_addtid", "ds_write_addtid", "s_movrel",
+               "v_movrel", "v_interp", "lds_param_load", "lds_direct_load", "global_load_lds", "s_ttracedata")
+
+
+def code_object_m0_misuse(hsaco):
+    """M0 in the gfx950 code object: every write must be the copy sequence `s_mov_b32 m0, sN; s_nop 0;
+    buffer_load_* ... lds` of the kernels' inline assembly, and no other instruction may read or write M0. Returns
+    the offending lines."""
+    llvm = os.path.join(ROCM, "llvm", "bin")
+    with tempfile.TemporaryDirectory() as td:
+        co = os.path.join(td, "k.co")
+        _run([os.path.join(llvm, "clang-offload-bundler"), "--unbundle", "--type=o", "--input=" + hsaco,
+              "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", "--output=" + co])
+        dis = _run([os.path.join(llvm, "llvm-objdump"), "-d", "--no-show-raw-insn", co]).stdout
+    ins = [l.split("//")[0].strip() for l in dis.splitlines()]
+    ins = [l for l in ins if l and not l.endswith(":") and not l.startswith("Disassembly") and " file format" not in l]
+    bad = []
+    for i, l in enumerate(ins):
+        op = l.split()[0]
+        if op.startswith(_M0_READERS):
+            bad.append(l)
+        elif "m0" in l.replace(",", " ").split()[1:]:
+            ok = (op == "s_mov_b32" and l.split()[1].rstrip(",") == "m0" and i + 2 < len(ins)
+                  and ins[i + 1].split()[0] == "s_nop" and ins[i + 2].startswith("buffer_load_") and ins[i + 2].endswith(" lds"))
+            if not ok:
+                bad.append(l)
+        elif op.startswith("buffer_load_") and l.endswith(" lds"):
+            if not (i >= 2 and ins[i - 2].startswith("s_mov_b32 m0,")):
+                bad.append(l)
+    return bad
+
+
 def build(verbose=False):
     os.makedirs(OUT, exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
@@ -64,6 +98,10 @@ def build(verbose=False):
         if calls:
             os.remove(co)
             raise RuntimeError(f"{co}: a kernel calls an outlined function ({calls[0]}); force-inline it")
+        m0 = code_object_m0_misuse(co)
+        if m0:
+            os.remove(co)
+            raise RuntimeError(f"{co}: M0 used outside the kernels' copy sequences ({m0[0]})")
     # the allocation-free entry is single-source HIP (its device array is registered with the runtime at load time)
     noalloc_o = os.path.join(OUT, "fmha_noalloc.o")
     _run([hipcc, *HIP_FLAGS, "-fPIC", "-c", os.path.join(CSRC, "fmha_noalloc.hip"), "-o", noalloc_o])

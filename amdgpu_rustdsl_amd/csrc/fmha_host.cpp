@@ -12,12 +12,13 @@
 #include <cstdint>
 #include <cstring>
 #include <atomic>
+#include <cstdlib>
 
 #include "../../include/fmha_mxfp8.h"
 #include "module_cache.h"
 
 static_assert(sizeof(fmha_mxfp8_args) == 656, "kernarg size (vs128_abi.h:126)");
-static_assert(sizeof(fmha_mxfp8_params) == 176, "params layout (lib.py mirrors it)");
+static_assert(sizeof(fmha_mxfp8_params) == 192, "params layout (lib.py mirrors it)");
 static_assert(offsetof(fmha_mxfp8_args, ptr_o) == 0x000, "ptr_o");
 static_assert(offsetof(fmha_mxfp8_args, ptr_q) == 0x010, "ptr_q");
 static_assert(offsetof(fmha_mxfp8_args, ptr_k) == 0x020, "ptr_k");
@@ -193,11 +194,16 @@ int rules_grid(const fmha_mxfp8_args& a, uint32_t gx, uint32_t gy, int rows_per_
     return FMHA_OK;
 }
 
-// The workspace slot turn of the KV split (see the slots in fmha_fwd_hd128_mxfp8_auto); shared by every call
-std::atomic<uint64_t> g_ws_turn{0};
-
 // Compute units of the current device (the causal pairing pays off only when the unpaired grid exceeds them), cached
+// FMHA_MXFP8_CU_COUNT (a positive integer) replaces the device's count: the CU-dependent rules (the KV fill, the
+// causal pairing, the causal split-tile choice) and so the output bits can then be checked for another part's count,
+// also on a machine without a GPU.
 int cu_count() {
+    static const int env = [] {
+        const char* e = std::getenv("FMHA_MXFP8_CU_COUNT");
+        return e ? std::atoi(e) : 0;
+    }();
+    if (env > 0) return env;
     static std::atomic<int> cache[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
@@ -459,8 +465,12 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
         while (sub > 1 && workspace_bytes < fmha_mxfp8_workspace_bytes(B, H, S, (int)(splits * sub))) sub /= 2;
         parts = splits * sub;
     }
+    if (path == FMHA_PATH_KVSPLIT && parts * B * S * H * 512 >= (1LL << 32))
+        // a kernel-contract limit (32-bit partial offsets), checked with or without no_check
+        return fail(err, errlen, FMHA_ERR_KA_RANGE, "GV-HOST-KA-RANGE", "ka(0x284) outside contract (partials of 4 GiB or more)");
     if (path_out) *path_out = path;
-    if (splits_out) *splits_out = path == FMHA_PATH_KVSPLIT ? (int)parts : 0;
+    if (splits_out) *splits_out = path == FMHA_PATH_KVSPLIT ? splits : 0;
+    if (p->partials_out) *p->partials_out = path == FMHA_PATH_KVSPLIT ? (int32_t)parts : 0;
     const uint32_t gy = (uint32_t)H;
     if (path == FMHA_PATH_VS128 || path == FMHA_PATH_T128) {
         a.ptr_lse = p->lse;
@@ -507,7 +517,8 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
     size_t nslots = workspace_bytes / stride;
     if (nslots < 1) nslots = 1;
     if (nslots > FMHA_WORKSPACE_SLOTS) nslots = FMHA_WORKSPACE_SLOTS;
-    const size_t slot = nslots > 1 ? (size_t)(g_ws_turn.fetch_add(1, std::memory_order_relaxed) % nslots) : 0u;
+    size_t slot = 0;
+    if (nslots > 1 && p->ws_turn) slot = (size_t)((*p->ws_turn)++ % nslots);
     uint8_t* ohat = (uint8_t*)workspace + slot * stride;
     uint8_t* lse = ohat + (size_t)parts * rows_total * 512;
     fmha_mxfp8_kvsplit_args ka;

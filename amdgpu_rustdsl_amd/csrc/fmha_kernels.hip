@@ -301,12 +301,17 @@ __device__ inline void lds_write4(uint32_t off, uint32_t v) { *(LDS_AS uint32_t*
 // assembly so that the compiler does not see an LDS write: through the builtin it makes every later LDS read of the ring
 // wait for all outstanding copies (vmcnt(0)), which would expose their full latency once per phase. The ordering is
 // explicit instead: a copy is published by the barrier that follows the wait on its vmcnt (block_barrier_keep_dma).
-// M0 carries the LDS base; no compiler-generated code in these kernels uses M0.
+// M0 carries the LDS base and is declared clobbered. The compiler reserves M0 and keeps no value in it across an asm
+// statement of its own accord; build.py checks every built code object for it: each M0 write is one of these, right
+// before its copy, and no instruction the compiler emitted reads M0 (its readers: LDS copies, s_sendmsg, GWS, ds_append
+// and ds_consume, LDS-direct / interpolation and s_movrel / v_movrel).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   // "clobber list contains reserved registers: m0" (intended)
 __device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint32_t voff, uint32_t soff) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :
                  : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
-                 : "memory");
+                 : "memory", "m0");
 }
 
 // The same with 4 bytes per lane: lane L's bytes land at lds_base + 4 L.
@@ -314,8 +319,9 @@ __device__ inline void dma4(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, uint
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
                  :
                  : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
-                 : "memory");
+                 : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // The copies of one 128-key tile (K and V: 16 KiB each; K scales: 512 B; per-32-key V scales: 512 B) from HBM into
 // its LDS ring slots. K and V go by direct copies (buffer_load ... lds, dma below); the 512-thread kernels stage the

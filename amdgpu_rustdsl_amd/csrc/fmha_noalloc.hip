@@ -76,7 +76,9 @@ extern "C" int fmha_fwd_hd128_mxfp8_auto_noalloc(const fmha_mxfp8_params* p, voi
         int path = p->path;
         if (path < 0) path = fmha_mxfp8_select_path(p->B, p->H, p->S, p->SK, &splits);
         else if (path == FMHA_PATH_KVSPLIT) splits = p->splits > 0 ? p->splits : 4;
-        if (path == FMHA_PATH_KVSPLIT) need = fmha_mxfp8_workspace_bytes(p->B, p->H, p->S, splits);
+        // an invalid split count is left to the entry, which reports it (GV-HOST-PATH)
+        if (path == FMHA_PATH_KVSPLIT && (splits == 2 || splits == 4 || splits == 8))
+            need = fmha_mxfp8_workspace_bytes(p->B, p->H, p->S, splits);
     }
     if (need > (size_t)FMHA_NOALLOC_SCRATCH_BYTES) {
         fmha_internal::set_err(err, errlen,

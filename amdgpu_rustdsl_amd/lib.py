@@ -81,10 +81,11 @@ class Params(ctypes.Structure):
                 ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("HK", ctypes.c_int32), ("S", ctypes.c_int32), ("SK", ctypes.c_int32),
                 ("path", ctypes.c_int32), ("splits", ctypes.c_int32), ("causal", ctypes.c_int32),
                 ("f32_partials", ctypes.c_int32), ("v_seq32", ctypes.c_int32), ("softmax_scale", ctypes.c_float),
-                ("no_check", ctypes.c_int32), ("causal_pair", ctypes.c_int32), ("kv_fill", ctypes.c_int32)]
+                ("no_check", ctypes.c_int32), ("causal_pair", ctypes.c_int32), ("kv_fill", ctypes.c_int32),
+                ("ws_turn", ctypes.POINTER(ctypes.c_uint32)), ("partials_out", ctypes.POINTER(ctypes.c_int32))]
 
 
-assert ctypes.sizeof(Params) == 176 and ctypes.sizeof(Args) == 656 and ctypes.sizeof(KvsplitArgs) == 648 and ctypes.sizeof(CombineArgs) == 36
+assert ctypes.sizeof(Params) == 192 and ctypes.sizeof(Args) == 656 and ctypes.sizeof(KvsplitArgs) == 648 and ctypes.sizeof(CombineArgs) == 36
 
 _c, _i64, _sz, _cp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_char_p
 _P = ctypes.POINTER
@@ -194,26 +195,44 @@ def init():
     check(_L.fmha_mxfp8_init(buf, 512), buf)
 
 
-def run_auto(params, workspace=None, workspace_bytes=0, stream=None):
-    """fmha_fwd_hd128_mxfp8_auto; returns (path name, splits)."""
+class Ran(tuple):
+    """(path name, splits) of a one-call entry: the KV split's chunk count, as the reference op returns it. The
+    partials per row that ran (the chunks times the KV fill) are in ``.partials`` (0 off the KV split)."""
+
+    def __new__(cls, path, splits, partials):
+        r = super().__new__(cls, (path, splits))
+        r.partials = partials
+        return r
+
+
+def _run(entry, params, *args):
     buf = _errbuf()
     path, splits = ctypes.c_int(-1), ctypes.c_int(0)
-    rc = _L.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(params), workspace, workspace_bytes, stream, ctypes.byref(path),
-                                      ctypes.byref(splits), buf, 512)
+    own = not params.partials_out
+    parts = ctypes.c_int32(0)
+    if own:
+        params.partials_out = ctypes.pointer(parts)
+    try:
+        rc = entry(ctypes.byref(params), *args, ctypes.byref(path), ctypes.byref(splits), buf, 512)
+        n = params.partials_out[0]
+    finally:
+        if own:
+            params.partials_out = None
     check(rc, buf)
-    return PATH_NAMES[path.value], splits.value
+    return Ran(PATH_NAMES[path.value], splits.value, n)
+
+
+def run_auto(params, workspace=None, workspace_bytes=0, stream=None):
+    """fmha_fwd_hd128_mxfp8_auto; returns Ran (path name, splits; .partials)."""
+    return _run(_L.fmha_fwd_hd128_mxfp8_auto, params, workspace, workspace_bytes, stream)
 
 
 NOALLOC_SCRATCH_BYTES = 33816576   # FMHA_NOALLOC_SCRATCH_BYTES
 
 
 def run_auto_noalloc(params, stream=None):
-    """fmha_fwd_hd128_mxfp8_auto_noalloc (no workspace argument); returns (path name, splits)."""
-    buf = _errbuf()
-    path, splits = ctypes.c_int(-1), ctypes.c_int(0)
-    rc = _L.fmha_fwd_hd128_mxfp8_auto_noalloc(ctypes.byref(params), stream, ctypes.byref(path), ctypes.byref(splits), buf, 512)
-    check(rc, buf)
-    return PATH_NAMES[path.value], splits.value
+    """fmha_fwd_hd128_mxfp8_auto_noalloc (no workspace argument); returns Ran (path name, splits; .partials)."""
+    return _run(_L.fmha_fwd_hd128_mxfp8_auto_noalloc, params, stream)
 
 
 def quantize_rows(x, q, scale, rows, mul, bytes_x, bytes_q, bytes_scale, stream=None):

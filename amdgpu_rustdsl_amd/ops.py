@@ -2,6 +2,7 @@
 (python/amdgpu_jit/ops.py:88-143): same arguments, layouts, path names and errors, over the C ABI of
 include/fmha_mxfp8.h (``amdgpu_rustdsl_amd.lib``). torch is used for device memory and the current stream only.
 """
+import ctypes
 import math
 
 import torch
@@ -44,18 +45,21 @@ _workspace = {}
 
 
 def _ws(device, stream, nbytes):
-    """Persistent KV-split workspace per (device, stream), grown on demand (ops.py:73-85)."""
+    """Persistent KV-split workspace per (device, stream), grown on demand (ops.py:73-85), with the turn word of its
+    slots (host memory, owned by this op: calls on one stream take the slots in turn)."""
     key = (device, stream)
-    buf = _workspace.get(key)
-    if buf is None or buf.numel() < nbytes:
-        buf = _workspace[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
-    return buf
+    ent = _workspace.get(key)
+    if ent is None or ent[0].numel() < nbytes:
+        ent = _workspace[key] = (torch.empty(nbytes, dtype=torch.uint8, device=device), ctypes.c_uint32(0))
+    return ent
 
 
 def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", splits=None, specialize=True, stream=None, check=True,
                    lse=None, causal=False, partials="fp16", softmax_scale=None, causal_pair="auto", kv_fill=True):
-    """Attention forward on MXFP8 inputs with head dim 128, written into ``out``; returns the (path, splits) that ran
-    (for the KV split, the partials per row: the chunks times the blocks each chunk was spread over).
+    """Attention forward on MXFP8 inputs with head dim 128, written into ``out``; returns the (path, splits) that ran,
+    splits being the KV split's chunk count as in the reference op (0 off the KV split). The returned tuple's
+    ``.partials`` gives the partials per row that ran: the chunks times the blocks each chunk was spread over (the
+    KV fill below).
 
     Scores are base-2: the kernels compute softmax2(q . k) over dequantised q and k, so a caller that wants the usual
     softmax(q k^T / sqrt(128)) multiplies q by log2(e) / sqrt(128) before quantising it (``fmha_fwd_bf16_via_mxfp8``
@@ -79,7 +83,9 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
     has the same work; "auto" pairs when the unpaired grid exceeds the device's CUs (same output bits either way);
     ``kv_fill`` (default True): a KV split whose grid would leave CUs idle spreads each chunk's keys over up to 8
     blocks (``lib.kv_partials``), the combine merging every block's partial; False keeps the reference's one block
-    per chunk.
+    per chunk. The fill changes the fp32 rounding order (each partial quantises P against its own running maximum),
+    so its output bits differ from the reference grid's by a few ULP; which fill runs depends on the device's CU
+    count.
     """
     pair_modes = {"auto": 0, True: 1, False: 2}
     if causal_pair not in pair_modes:
@@ -144,7 +150,9 @@ def fmha_fwd_mxfp8(q, k, v, q_scale, k_scale, v_scale, out, *, path="auto", spli
         slotted = lib.WORKSPACE_SLOTS * ((ws_bytes + 255) // 256 * 256)
         if slotted <= 512 << 20:
             ws_bytes = slotted
-        ws = _ws(dev, st, ws_bytes).data_ptr()
+        buf, turn = _ws(dev, st, ws_bytes)
+        ws = buf.data_ptr()
+        p.ws_turn = ctypes.pointer(turn)
     with torch.cuda.device(dev):
         return lib.run_auto(p, ws, ws_bytes, st)
 

@@ -19,6 +19,7 @@ kernel is launched alone through the C-ABI launcher, timed with HIP events on it
 inputs, all host cores, on a bounded sample of the same workload (rank 0, N = 1).
 """
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -146,14 +147,23 @@ def main():
     p.path = -1 if path == "auto" else lib.PATH_IDS[path]
     p.splits, p.causal = splits or 0, int(causal)
     # the KV split's workspace as the op sizes it: the entry's workspace slots of the partials that ran
-    ws_bytes = lib.WORKSPACE_SLOTS * ((lib.workspace_bytes(B, H, S, used[1]) + 255) // 256 * 256) if used[0] == "kvsplit" else 0
+    ws_bytes = lib.WORKSPACE_SLOTS * ((lib.workspace_bytes(B, H, S, used.partials) + 255) // 256 * 256) if used[0] == "kvsplit" else 0
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    turn = ctypes.c_uint32(0)   # the caller-owned turn word of the workspace slots
+    p.ws_turn = ctypes.pointer(turn)
     st = stream.cuda_stream
 
-    def step():
-        return lib.run_auto(p, ws.data_ptr(), ws_bytes, st)
+    # one step = one call of the C entry; its arguments are built once (ctypes objects cost microseconds per call,
+    # which a short timed window would otherwise see as GPU idle time before the first launch)
+    entry = lib.raw.fmha_fwd_hd128_mxfp8_auto
+    po, so, errbuf = ctypes.c_int(-1), ctypes.c_int(0), ctypes.create_string_buffer(512)
+    call_args = (ctypes.byref(p), ws.data_ptr(), ws_bytes, st, ctypes.byref(po), ctypes.byref(so), errbuf, 512)
 
-    assert step() == used
+    def step():
+        if entry(*call_args) != 0:
+            raise RuntimeError(f"fmha_fwd_hd128_mxfp8_auto: {errbuf.value.decode()}")
+
+    assert lib.run_auto(p, ws.data_ptr(), ws_bytes, st) == used
     torch.cuda.synchronize()
     # the configs[1] line is quoted with the LSE saved: the natural-log LSE output (vs128 / t128) is on for the timed
     # steps of the full-sequence paths
@@ -161,7 +171,7 @@ def main():
     if used[0] in ("vs128", "t128"):
         lse = torch.empty(B, H, S, dtype=torch.float32, device=dev)
         p.lse = lse.data_ptr()
-        assert step() == used
+        assert lib.run_auto(p, ws.data_ptr(), ws_bytes, st) == used
 
     def timed(fn, n):
         """Event time (ms) of n calls of fn on the stream, bracketed by synchronisations; the wall time beside it."""
@@ -236,7 +246,7 @@ def main():
         "dtype": "e4m3 (MXFP8, E8M0/32 scales, fp32 accumulate)",
         "data": "synthetic: N(0,1) Q/K/V quantised to MXFP8 like the reference's REF_DATA=normal generator, drawn on the GPU",
         "config": {"workload": f"fmha_fwd_hd128_mxfp8_auto {desc}", "B": B, "H": H, "HK": HK, "S": S, "SK": SK,
-                   "causal": causal, "path": used[0], "splits": used[1], "kv_chunks": (splits or lib.select_path(B, H, S, SK)[1]) if used[0] == "kvsplit" else None, "lse": lse is not None,
+                   "causal": causal, "path": used[0], "splits": used[1], "kv_partials": used.partials if used[0] == "kvsplit" else None, "lse": lse is not None,
                    "pct_mxfp8_peak": round(100 * tflops / PEAK_MXFP8_TFLOPS, 2)},
         "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": PEAK_MXFP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(kern_tflops / PEAK_MXFP8_TFLOPS, 4), "traffic": traffic,
@@ -246,7 +256,7 @@ def main():
         # the KV split is HBM-bound (about 226 FLOP per byte at config 5, below the ridge of 5.0e15 / 8e12): its
         # split kernel reads Q, K, V and their scales once and writes the fp16 partial rows and LSE words
         rows = B * S * H
-        split_bytes = rows * (128 + 4) + 2 * B * SK * HK * 128 + B * SK * HK * 4 + used[1] * rows * (256 + 4)
+        split_bytes = rows * (128 + 4) + 2 * B * SK * HK * 128 + B * SK * HK * 4 + used.partials * rows * (256 + 4)
         gbs = split_bytes / (kern_ms * 1e-3) / 1e9
         line["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                             "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "algorithmic_bytes": split_bytes,

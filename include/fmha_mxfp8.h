@@ -280,17 +280,27 @@ typedef struct fmha_mxfp8_params {
     int32_t kv_fill;           /* KV split only (extension): 0 = each chunk spread over the blocks that
                                   fmha_mxfp8_kv_partials names, as far as the workspace holds their partials;
                                   1 = the reference's chunks only (one block per chunk and query tile) */
+    uint32_t* ws_turn;         /* KV split only (extension), optional: a turn word the caller owns (host memory). With a
+                                  workspace of several slots the call uses slot *ws_turn % slots and increments the
+                                  word; NULL = slot 0. Calls that share a word take the slots in turn; callers with
+                                  their own words (and workspaces) never affect each other's slots. */
+    int32_t* partials_out;     /* optional output (extension): the KV split's partials per row that ran (the chunks
+                                  times the KV fill; 0 off the KV split) */
 } fmha_mxfp8_params;
 
 /* fmha_fwd_hd128_mxfp8_auto: dispatch + validate + launch (+ combine), all on
  * `stream`, no host synchronisation. `workspace` (device, >= the value of
- * fmha_mxfp8_workspace_bytes for the chosen split) is needed only when the KV
- * split runs; it may be NULL otherwise. On return *path_out / *splits_out
- * (may be NULL) name what ran. Mirrors python/amdgpu_jit/ops.py:88-143.
+ * fmha_mxfp8_workspace_bytes for the partials that run, p->partials_out) is
+ * needed only when the KV split runs; it may be NULL otherwise. On return
+ * *path_out / *splits_out (may be NULL) name what ran: the path and, for the
+ * KV split, its chunk count (2, 4 or 8), as the reference op returns them.
+ * Mirrors python/amdgpu_jit/ops.py:88-143. The library keeps no mutable state
+ * between calls (the compiled-module and CU-count caches aside).
  * Extension: a workspace of k >= 2 times that size (each copy rounded up to 256 B) is used as min(k,
- * FMHA_WORKSPACE_SLOTS) slots taken in turn by consecutive calls, so that a call's split kernel does not write the
- * lines the previous call's combine has just read (on MI355X that costs up to a quarter of the call: B1H8S2048 with
- * 4 splits runs 25.6 us per call on one slot, 19.1 us on four). The minimum size keeps the reference's behaviour. */
+ * FMHA_WORKSPACE_SLOTS) slots taken in turn through the caller's p->ws_turn word, so that a call's split kernel does
+ * not write the lines the previous call's combine has just read (on MI355X that costs up to a quarter of the call:
+ * B1H8S2048 with 4 splits runs 25.6 us per call on one slot, 19.1 us on four). The minimum size, or no turn word,
+ * keeps the reference's behaviour. */
 #define FMHA_WORKSPACE_SLOTS 4u
 int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_t workspace_bytes,
                               void* stream, int* path_out, int* splits_out, char* err, size_t errlen);

@@ -150,3 +150,72 @@ def fp64_rows(inp, rows):
             w = np.exp2(s - s.max(1, keepdims=True))
             out[b, :, h] = (w / w.sum(1, keepdims=True)) @ v[b, :, h // g]
     return out, gap, mag
+
+
+def causal_rows(inp, rows):
+    """float64 attention of the listed rows under the bottom-right causal mask (base-2 scores; a row with no visible
+    key gives zeros), each row's visible-key count, and per element the largest change one e4m3 step of one key's P
+    can make: max_k w_k 2^-3 |v_k,d - o_d| over the visible keys k (w_k the row's float64 softmax weights; 2^-3 is an
+    e4m3 step relative to the value at the bottom of its binade). Returns (out [B, n, H, 128], vis [n],
+    flip [B, n, H, 128])."""
+    sel = oracle.row_list(inp.S, rows)
+    q, k, v = _dequant(inp)
+    B, H, HK, S, SK = inp.B, inp.H, inp.HK, inp.S, inp.SK
+    g = H // HK
+    vis = np.clip(sel.astype(np.int64) + SK - S + 1, 0, SK)
+    out = np.zeros((B, sel.size, H, D))
+    flip = np.zeros((B, sel.size, H, D))
+    for b in range(B):
+        for h in range(H):
+            s = q[b, sel, h] @ k[b, :, h // g].T
+            s[np.arange(SK)[None, :] >= vis[:, None]] = -np.inf
+            live = vis > 0
+            s = s[live]
+            w = np.exp2(s - s.max(1, keepdims=True))
+            w /= w.sum(1, keepdims=True)
+            vv = v[b, :, h // g]
+            o = w @ vv
+            out[b, live, h] = o
+            # max over keys of w_k |v_k - o| per dim, in blocks of rows to bound the temporary
+            f = np.zeros_like(o)
+            for r0 in range(0, o.shape[0], 16):
+                blk = w[r0:r0 + 16, :, None] * np.abs(vv[None, :, :] - o[r0:r0 + 16, None, :])
+                f[r0:r0 + 16] = blk.max(1)
+            flip[b, live, h] = f * 2.0 ** -3
+    return out, vis, flip
+
+
+def causal_bar(inp, out, emu, rows):
+    """The causal bar against the oracle alone (no kernel output on the other side):
+    - element-wise closeness to the recipe's emulation: within 0.05 on rows that see at least 64 keys (as without the
+      mask), within 0.25 on rows with fewer, whose outputs rest on a few keys;
+    - an element outside the harness tolerance (ref_host.cpp:466: |err| > 0.05 + 0.05 |ref|) that the emulation keeps
+      inside it must differ from the emulation by no more than one e4m3 step of one key's P can move it (the MFMA's
+      inexact sums can carry a P value across a rounding step), and such elements may lie in at most 2 % of the rows.
+    Returns a dict of the figures (for the log) and the list of violations."""
+    sel = oracle.row_list(inp.S, rows)
+    ref, vis, flip = causal_rows(inp, rows)
+    shape = (inp.B, inp.S, inp.H, D)
+    o = oracle.bf16_to_f32(out.reshape(shape)[:, sel]).astype(np.float64)
+    e = oracle.bf16_to_f32(emu.reshape(shape)[:, sel]).astype(np.float64)
+    d = np.abs(o - e)
+    many = vis >= 64
+    tol = lambda x: np.abs(x - ref) <= 0.05 + 0.05 * np.abs(ref)
+    extra = ~tol(o) & tol(e)
+    explained = d <= 1.5 * flip + 2.0 ** -8 * np.abs(ref) + 1e-4
+    rows_extra = int(extra.any(axis=3).sum())   # attention rows (b, query, h) holding such an element
+    nrows = inp.B * sel.size * inp.H
+    fig = {"max_abs_many": float(d[:, many].max()) if many.any() else 0.0,
+           "max_abs_few": float(d[:, ~many].max()) if (~many).any() else 0.0,
+           "bad_ours": int((~tol(o)).sum()), "bad_emulation": int((~tol(e)).sum()), "extra": int(extra.sum()),
+           "extra_unexplained": int((extra & ~explained).sum()), "extra_rows": rows_extra, "rows": nrows}
+    viol = []
+    if fig["max_abs_many"] > 0.05:
+        viol.append("max_abs over rows with >= 64 visible keys")
+    if fig["max_abs_few"] > 0.25:
+        viol.append("max_abs over rows with < 64 visible keys")
+    if fig["extra_unexplained"]:
+        viol.append("elements outside the tolerance beyond one P step")
+    if rows_extra > 0.02 * nrows + 1:
+        viol.append("too many rows with extra elements outside the tolerance")
+    return fig, viol

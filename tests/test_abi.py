@@ -441,3 +441,128 @@ def test_kv_partials_rule(shape, chunks, parts):
     sub blocks stay within the CU count (256 on MI355X; the value the library assumes without a device) and every
     key range keeps at least 4 key tiles."""
     assert lib.kv_partials(*shape, chunks) == parts
+
+
+def test_workspace_turn_is_the_callers():
+    """The KV split's workspace slot comes from the caller's own turn word (params.ws_turn), incremented once per call
+    that reaches the slot choice: two threads with their own words and workspaces see exactly their own calls, in
+    order, whatever the other does; no word (NULL) is slot 0 and leaves nothing behind. Runs without a GPU: the call
+    then fails at the launch, after the slot choice."""
+    import threading
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("the calls would launch on the GPU")
+    n = 200
+    need = lib.workspace_bytes(1, 8, 128, lib.kv_partials(1, 8, 128, 4096, 4))
+    words = [ctypes.c_uint32(0), ctypes.c_uint32(1000)]
+    codes = [set(), set()]
+
+    def worker(i):
+        p = _params(path=2, splits=4, SK=4096)
+        p.ws_turn = ctypes.pointer(words[i])
+        err = ctypes.create_string_buffer(256)
+        po, so = ctypes.c_int(-1), ctypes.c_int(-1)
+        for _ in range(n):
+            codes[i].add(lib.raw.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(p), 0x10000 * (i + 1), 4 * need + 1024, None,
+                                                           ctypes.byref(po), ctypes.byref(so), err, 256))
+    ts = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert words[0].value == n and words[1].value == 1000 + n
+    assert codes[0] <= {lib.FMHA_ERR_NO_DEVICE, lib.FMHA_ERR_HIP} and codes[1] <= {lib.FMHA_ERR_NO_DEVICE, lib.FMHA_ERR_HIP}
+    # one slot's worth of workspace: no turn taken
+    p = _params(path=2, splits=4, SK=4096)
+    w = ctypes.c_uint32(7)
+    p.ws_turn = ctypes.pointer(w)
+    err = ctypes.create_string_buffer(256)
+    po, so = ctypes.c_int(-1), ctypes.c_int(-1)
+    lib.raw.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(p), 0x10000, need, None, ctypes.byref(po), ctypes.byref(so), err, 256)
+    assert w.value == 7
+
+
+def test_auto_reports_chunks_and_partials():
+    """*splits_out is the KV split's chunk count (the reference op's return value, python/amdgpu_jit/ops.py:143);
+    params.partials_out receives the partials per row that run (chunks x the KV fill). Checked without a GPU: both are
+    written before the launch."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("the call would launch on the GPU")
+    for kv_fill, parts in ((0, 32), (1, 8)):
+        p = _params(path=2, splits=8, S=128, SK=16384, kv_fill=kv_fill)
+        got = ctypes.c_int32(-1)
+        p.partials_out = ctypes.pointer(got)
+        err = ctypes.create_string_buffer(256)
+        po, so = ctypes.c_int(-1), ctypes.c_int(-1)
+        need = lib.workspace_bytes(1, 8, 128, parts)
+        rc = lib.raw.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(p), 0x10000, need, None, ctypes.byref(po), ctypes.byref(so), err, 256)
+        assert rc in (lib.FMHA_ERR_NO_DEVICE, lib.FMHA_ERR_HIP), (rc, err.value)
+        assert (po.value, so.value, got.value) == (lib.PATH_KVSPLIT, 8, parts)
+    # a full-sequence path: no split, no partials
+    p = _params(path=0)
+    got = ctypes.c_int32(-1)
+    p.partials_out = ctypes.pointer(got)
+    lib.raw.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(p), None, 0, None, ctypes.byref(po), ctypes.byref(so), err, 256)
+    assert (so.value, got.value) == (0, 0)
+
+
+def test_unchecked_split_keeps_the_32bit_guard():
+    """params.no_check skips the buffer-extent rules, not the kernel contract's 32-bit partial offsets: a split whose
+    partials reach 4 GiB is refused either way."""
+    for no_check in (0, 1):
+        p = _params(path=2, splits=8, B=8, H=16, S=8192, SK=8192, kv_fill=1)   # 8 x 1 Mi rows x 512 B = 4 GiB
+        p.no_check = no_check
+        err = ctypes.create_string_buffer(256)
+        po, so = ctypes.c_int(-1), ctypes.c_int(-1)
+        rc = lib.raw.fmha_fwd_hd128_mxfp8_auto(ctypes.byref(p), 0x10000, 1 << 40, None, ctypes.byref(po), ctypes.byref(so), err, 256)
+        assert rc == lib.FMHA_ERR_KA_RANGE and b"4 GiB" in err.value, (no_check, rc, err.value)
+
+
+_CU_RULES = r"""
+import json, sys
+sys.path.insert(0, {root!r})
+from amdgpu_rustdsl_amd import lib
+print(json.dumps({{
+    "parts": [lib.kv_partials(1, 8, 128, 16384, 8), lib.kv_partials(1, 8, 512, 32768, 4), lib.kv_partials(1, 8, 2048, 2048, 4)],
+    "st": [lib.uses_split_tiles("vs128", 2, 8, 1024, 1024, causal=True), lib.uses_split_tiles("t128", 16, 8, 512, 512, causal=True)],
+}}))
+"""
+
+
+@pytest.mark.parametrize("cus,parts,st", [
+    # KV fill: blocks (S + 255) / 256 H B chunks, doubled while within the count and >= 4 key tiles per range;
+    # causal split tiles: refused for <= 8 key tiles when the 128-row grid ((S + 127) / 128 H B) exceeds the count
+    (None, [32, 16, 4], [True, False]),   # no device: 256, MI355X's count
+    ("256", [32, 16, 4], [True, False]),
+    ("304", [32, 16, 4], [True, False]),
+    ("128", [16, 8, 4], [True, False]),
+    ("80", [8, 4, 4], [False, False]),
+    ("1024", [32, 32, 4], [True, True]),
+])
+def test_cu_dependent_rules(cus, parts, st):
+    """The rules that follow the device's CU count (the KV fill, the causal split-tile choice), under
+    FMHA_MXFP8_CU_COUNT: the output bits of those paths follow the count, so other parts get other (equally checked)
+    orders."""
+    import json
+    import subprocess
+    import sys
+    env = dict(os.environ)
+    env.pop("FMHA_MXFP8_CU_COUNT", None)
+    if cus:
+        env["FMHA_MXFP8_CU_COUNT"] = cus
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = subprocess.run([sys.executable, "-c", _CU_RULES.format(root=root)], env=env, capture_output=True, text=True,
+                         check=True).stdout
+    got = json.loads(out.strip().splitlines()[-1])
+    assert got == {"parts": parts, "st": st}
+
+
+def test_code_objects_keep_m0_to_the_copies():
+    """M0 is written only by the kernels' own direct-copy sequences, and nothing the compiler emitted reads it
+    (build.py refuses other code objects)."""
+    from amdgpu_rustdsl_amd import build
+    path = os.path.join(os.path.dirname(lib.LIB_PATH), "fmha_mxfp8_gfx950.hsaco")
+    if not os.path.exists(path):
+        pytest.skip("not built")
+    assert build.code_object_m0_misuse(path) == []

@@ -69,7 +69,7 @@ def _run_path(gpu, inp, path):
     splits = 2 if path == "kvsplit" else None
     out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
     if used[0] == "kvsplit":
-        return out, (used[1], True), used, gpu_util.chunks(inp, path, splits)
+        return out, (used.partials, True), used, gpu_util.chunks(inp, path, splits)
     return out, (0, lib.uses_split_tiles(used[0], B, H, S, SK, inp.causal)), used, 0
 
 
@@ -192,11 +192,11 @@ def test_split_vs_full(gpu, case):
     rows = oracle.first_and_last(S, 64)
     full = gpu_util.run_direct(inp, gpu, "vs128")
     split, used, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits)
-    assert used == ("kvsplit", lib.kv_partials(B, H, S, SK, splits))
+    assert used == ("kvsplit", splits) and used.partials == lib.kv_partials(B, H, S, SK, splits)
     sel = lambda x: x.reshape(B, S, H, 128)[:, rows]
     ours = _diff(sel(split), sel(full))
     emu_full = oracle.emulate(inp, rows=rows)
-    emu_split = oracle.emulate(inp, splits=used[1], rows=rows, split_tiles=True)
+    emu_split = oracle.emulate(inp, splits=used.partials, rows=rows, split_tiles=True)
     emu_ref_split = oracle.emulate(inp, splits=splits, rows=rows)
     want = _diff(sel(emu_split), sel(emu_full))          # the same pair of orders, emulated
     ref = _diff(sel(emu_ref_split), sel(emu_full))       # the reference kernels' pair

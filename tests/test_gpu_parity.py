@@ -9,6 +9,8 @@ It cannot be bit-identical: the gfx950 scaled fp8 MFMA does not sum its 64 produ
 ~3e-4 of the largest product), which moves the fp8 rounding of some P values; the emulation sums exactly. The
 element-wise bound therefore is a fraction of the reference's own error, not zero.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -58,7 +60,7 @@ def test_parity(gpu, case):
     print(f"[case] {name}", flush=True)
     inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
     out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
-    used_splits = used[1] if used[0] == "kvsplit" else 0
+    used_splits = used.partials if used[0] == "kvsplit" else 0
     # the reference's sample (the first 64 rows of every (b, h)) and the last 64: the last query tile and the tail
     rows = oracle.first_and_last(S, ROWS)
     emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0], ref_splits=gpu_util.chunks(inp, path, splits))
@@ -98,12 +100,13 @@ def test_parity_causal(gpu, case):
     emu, ref_stats = _emulated_bar(inp, 0, rows=rows, path=used[0])
     stats = oracle.check_fp64(inp, out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
-    print(f"[case] {name} path={used} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
+    fig, viol = gpu_util.causal_bar(inp, out, emu, rows)
+    print(f"[case] {name} path={used} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp} causal-bar={fig}", flush=True)
     assert not np.isnan(oracle.bf16_to_f32(out)).any()
     assert stats["bad"] <= ref_stats["bad"]
     assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
     assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
-    assert cmp["max_abs"] <= 0.25, cmp   # causal: looser than the 0.05 of the unmasked cases (observed up to 0.094)
+    assert not viol, (viol, fig)   # per-row element bound by visible-key count (gpu_util.causal_bar)
     if S > SK:
         o = oracle.bf16_to_f32(out).reshape(B, S, H, 128)
         assert (o[:, : S - SK] == 0).all()   # query i sees keys t <= i + SK - S: none for i < S - SK
@@ -125,9 +128,9 @@ def test_parity_f32_partials(gpu, case):
     print(f"[case] f32 partials {name}", flush=True)
     inp = oracle.Inputs(B, H, S, SK, HK=HK)
     out, used, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits, partials="fp32")
-    assert used == ("kvsplit", lib.kv_partials(B, H, S, SK, splits))
+    assert used == ("kvsplit", splits) and used.partials == lib.kv_partials(B, H, S, SK, splits)
     out16, _, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits)
-    emu, ref_stats = _emulated_bar(inp, used[1], f32_partials=True, ref_splits=splits)
+    emu, ref_stats = _emulated_bar(inp, used.partials, f32_partials=True, ref_splits=splits)
     stats = oracle.check_fp64(inp, out, rows=ROWS)
     stats16 = oracle.check_fp64(inp, out16, rows=ROWS)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, min(ROWS, S))
@@ -159,7 +162,7 @@ def test_parity_v_seq32(gpu, case):
     inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal, v_seq32=True)
     out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
     assert used[0] == path
-    used_splits = used[1] if used[0] == "kvsplit" else 0
+    used_splits = used.partials if used[0] == "kvsplit" else 0
     rows = oracle.first_and_last(S, 128 if causal else ROWS)
     emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0], ref_splits=gpu_util.chunks(inp, path, splits))
     stats = oracle.check_fp64(inp, out, rows=rows)
@@ -217,8 +220,8 @@ def test_parity_split_tiles(gpu, case):
     inp = oracle.Inputs(B, H, S, SK, HK=HK, v_seq32=opt.get("v_seq32", False))
     f32 = opt.get("partials") == "fp32"
     out, used, _ = gpu_util.run(inp, gpu, path="kvsplit", splits=splits, partials=opt.get("partials", "fp16"))
-    assert used == ("kvsplit", lib.kv_partials(B, H, S, SK, splits))
-    emu, ref_stats = _emulated_bar(inp, used[1], rows=S, f32_partials=f32, ref_splits=splits)
+    assert used == ("kvsplit", splits) and used.partials == lib.kv_partials(B, H, S, SK, splits)
+    emu, ref_stats = _emulated_bar(inp, used.partials, rows=S, f32_partials=f32, ref_splits=splits)
     stats = oracle.check_fp64(inp, out, rows=S)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, S)
     print(f"[case] split tiles {name} ours={stats} emulated-reference={ref_stats} vs-emulation={cmp}", flush=True)
@@ -251,7 +254,7 @@ def test_parity_qk_scale(gpu, case):
     inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal, v_seq32=vs32, qk_scale=scale)
     out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
     assert used[0] == path
-    used_splits = used[1] if used[0] == "kvsplit" else 0
+    used_splits = used.partials if used[0] == "kvsplit" else 0
     rows = S if path == "kvsplit" else oracle.first_and_last(S, 128 if causal else ROWS)
     emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0], ref_splits=gpu_util.chunks(inp, path, splits))
     stats = oracle.check_fp64(inp, out, rows=rows)
@@ -338,10 +341,13 @@ def test_parity_vs128_split_tiles(gpu, case):
     assert stats["bad"] <= ref_stats["bad"]
     assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
     assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
-    # under the causal mask a looser element-wise bound, as in test_parity_causal: in the first rows a few keys carry
-    # the whole weight, so one fp8 rounding of P that the MFMA's inexact sum moves shifts an output by a few % of |V|
-    # (observed up to 0.094 over the causal cases)
-    assert cmp["max_abs"] <= (0.25 if causal else 0.05), cmp
+    if causal:
+        # under the mask the per-row element bound of test_parity_causal (gpu_util.causal_bar)
+        fig, viol = gpu_util.causal_bar(inp, out, emu, rows)
+        print(f"[case] vs128 split tiles {name} causal-bar={fig}", flush=True)
+        assert not viol, (viol, fig)
+    else:
+        assert cmp["max_abs"] <= 0.05, cmp
     if not causal:
         # the direct vs128 launcher keeps the 256-row kernel its grid names (the single-stream order), correct here too
         import ctypes, math, torch
@@ -394,18 +400,17 @@ def test_causal_pairing(gpu, case):
     emu, ref_stats = _emulated_bar(inp, 0, rows=rows, path=used[0])
     stats = oracle.check_fp64(inp, paired, rows=rows)
     cmp = gpu_util.compare_to_emulation(paired, emu, inp, rows)
-    print(f"[case] causal pairing {name} path={used} ours={stats} emulated={ref_stats} vs-emulation={cmp}", flush=True)
-    bad_bar = ref_stats["bad"]
-    if "single_wave" in name:
-        # On these large causal grids both hardware kernels leave a few more elements outside the harness tolerance
-        # than the exact emulation does (B16H8S512: 13 against 9, for the split-tile kernel as for this one; the
-        # first rows' outputs rest on a few keys, whose P the MFMA's inexact sums can move across a rounding step).
-        # The bar for the routing: no more than the split-tile kernel that these shapes ran on before.
-        bad_bar = max(bad_bar, oracle.check_fp64(inp, gpu_util.run_direct(inp, gpu, "t128_split_tiles"), rows=rows)["bad"])
-    assert stats["bad"] <= bad_bar
+    fig, viol = gpu_util.causal_bar(inp, paired, emu, rows)
+    print(f"[case] causal pairing {name} path={used} ours={stats} emulated={ref_stats} vs-emulation={cmp} causal-bar={fig}",
+          flush=True)
+    # Bad elements: on the large causal grids the hardware kernels can leave a few more elements outside the harness
+    # tolerance than the exact emulation (B16H8S512: 13 against 9): the first rows' outputs rest on a few keys, whose
+    # P the MFMA's inexact sums can carry across an e4m3 rounding step. causal_bar admits such an element only where
+    # one step of one key's P explains its distance from the emulation, in at most 2 % of the rows.
+    assert stats["bad"] <= ref_stats["bad"] + fig["extra"]
     assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
     assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
-    assert cmp["max_abs"] <= 0.25, cmp
+    assert not viol, (viol, fig)
 
 
 # Extension: KV-split workspace slots. A workspace of k times the reference's size is used as min(k, 4) slots taken in
@@ -421,8 +426,9 @@ def test_workspace_slots(gpu):
     used = lib.select_path(B, H, S, SK)
     assert used[0] == "kvsplit"
     # (sized for the partials the entry writes with the fill, so that every workspace below runs the same partials)
-    used = (used[0], lib.kv_partials(B, H, S, SK, used[1]))
-    need = lib.workspace_bytes(B, H, S, used[1])
+    parts = lib.kv_partials(B, H, S, SK, used[1])
+    need = lib.workspace_bytes(B, H, S, parts)
+    turn = ctypes.c_uint32(0)
     st = torch.cuda.current_stream(gpu).cuda_stream
 
     def call(ws, nbytes):
@@ -434,7 +440,9 @@ def test_workspace_slots(gpu):
         p.bytes_q_descale, p.bytes_k_descale, p.bytes_v_descale = ops._cap(qs), ops._cap(ks), ops._cap(vs)
         p.B, p.H, p.HK, p.S, p.SK = B, H, inp.HK, S, SK
         p.path, p.splits = -1, 0
-        assert lib.run_auto(p, ws.data_ptr(), nbytes, st) == used
+        p.ws_turn = ctypes.pointer(turn)
+        ran = lib.run_auto(p, ws.data_ptr(), nbytes, st)
+        assert ran == used and ran.partials == parts
         torch.cuda.synchronize()
         return out.view(torch.int16).cpu().numpy()
 
@@ -467,10 +475,10 @@ def test_parity_kv_fill(gpu, case):
     chunks = gpu_util.chunks(inp, path, splits)
     out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits)
     ref_out, ref_used, _ = gpu_util.run(inp, gpu, path=path, splits=splits, kv_fill=False)
-    assert used == ("kvsplit", lib.kv_partials(B, H, S, SK, chunks)) and used[1] > chunks
-    assert ref_used == ("kvsplit", chunks)
+    assert used == ("kvsplit", chunks) and used.partials == lib.kv_partials(B, H, S, SK, chunks) and used.partials > chunks
+    assert ref_used == ("kvsplit", chunks) and ref_used.partials == chunks
     rows = oracle.first_and_last(S, ROWS)
-    emu, ref_stats = _emulated_bar(inp, used[1], rows=rows, ref_splits=chunks)
+    emu, ref_stats = _emulated_bar(inp, used.partials, rows=rows, ref_splits=chunks)
     stats = oracle.check_fp64(inp, out, rows=rows)
     stats_chunks = oracle.check_fp64(inp, ref_out, rows=rows)
     cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)

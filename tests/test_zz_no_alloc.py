@@ -42,7 +42,7 @@ def _both(gpu, inp, path=-1, splits=0):
     p.o = out_na.data_ptr()
     got_na = lib.run_auto_noalloc(p, st)
     torch.cuda.synchronize()
-    assert got_ref == got_na
+    assert got_ref == got_na and got_ref.partials == got_na.partials
     a = out_ref.view(torch.int16).cpu().numpy()
     b = out_na.view(torch.int16).cpu().numpy()
     return got_na, a, b
@@ -61,6 +61,34 @@ def test_noalloc_matches_workspace_entry(gpu):
         print(f"[case] noalloc {name} path={used}", flush=True)
         assert not np.isnan(oracle.bf16_to_f32(b.view(np.uint16))).any()
         assert np.array_equal(a, b), f"{name}: {np.mean(a != b):.3g} of the elements differ"
+
+
+def test_noalloc_allocates_nothing(gpu):
+    """After a first call (which looks the scratch array up and loads the code objects), calls of the allocation-free
+    entry leave the device's free memory unchanged: no hipMalloc, no allocating library routine."""
+    inp = oracle.Inputs(1, 8, 128, 16384)
+    tensors = gpu_util.upload(inp, gpu)
+    st = torch.cuda.current_stream(gpu).cuda_stream
+    out = torch.empty((inp.B, inp.S, inp.H, 128), dtype=torch.bfloat16, device=gpu)
+    p = _params(inp, tensors, out, lib.PATH_KVSPLIT, 8)
+    lib.run_auto_noalloc(p, st)
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info(gpu)
+    for _ in range(20):
+        lib.run_auto_noalloc(p, st)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info(gpu)
+    assert free1 == free0, f"device free memory changed by {free0 - free1} bytes over 20 calls"
+
+
+def test_noalloc_rejects_bad_split_count(gpu):
+    """An invalid forced split count gets the entry's own error (GV-HOST-PATH), not the scratch-size one."""
+    p = lib.Params()
+    p.B, p.H, p.HK, p.S, p.SK, p.path, p.splits = 1, 8, 8, 128, 16384, lib.PATH_KVSPLIT, 16
+    err = ctypes.create_string_buffer(256)
+    po, so = ctypes.c_int(-1), ctypes.c_int(-1)
+    rc = lib.raw.fmha_fwd_hd128_mxfp8_auto_noalloc(ctypes.byref(p), None, ctypes.byref(po), ctypes.byref(so), err, 256)
+    assert rc == lib.FMHA_ERR_PATH and b"GV-HOST-PATH" in err.value
 
 
 def test_noalloc_rejects_oversized_split(gpu):
