@@ -30,7 +30,10 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
 # 256 registers per wave; left to choose, the compiler placed the QK MFMAs' S accumulators in AGPRs and moved all 64
 # back to VGPRs for the softmax every tile (80 v_accvgpr moves per tile in the loop). In the VGPR form other values
 # take the AGPRs and the loop has none. The other kernels fit in 256 VGPRs and compile to the same code either way.
-FMHA_FLAGS = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+# Kernel-argument preload: the first 9 dwords of scalar kernel parameters arrive in SGPRs at wave launch (the combines,
+# whose 36-byte layout is nine dwords of scalars); the attention kernels take one aggregate parameter, which is not
+# preloaded, and compile to the same code with or without it.
+FMHA_FLAGS = ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=9"]
 
 
 def _run(cmd):

@@ -51,6 +51,9 @@ namespace {
 #ifndef FMHA_PREFETCH
 #define FMHA_PREFETCH 2
 #endif
+#ifndef FMHA_KSDMA
+#define FMHA_KSDMA 0
+#endif
 
 constexpr int kD = 128;
 constexpr int kTile = 128;                    // keys per KV tile
@@ -747,7 +750,7 @@ struct Wave {
         v8i qf0;
         uint32_t ksw[4];
     };
-    template <int NA = 4, int KB0 = 0>
+    template <int NA = 4, int KB0 = 0, bool KSDMA = false>
     __device__ __forceinline__ void qk_prefetch(uint32_t kslot, Ring& ring, QkPre& pre) const {
         static_assert(DEPTH <= 2 * NA, "the prefetched operands are K fragments");
         const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
@@ -756,7 +759,7 @@ struct Wave {
         for (int i = 0; i < DEPTH; ++i) ring[i] = frag(kb, i / NA, 4096u * (uint32_t)(KB0 + i % NA));
         pre.qf0 = qfrag(0);
 #pragma unroll
-        for (int t4 = 0; t4 < NA; ++t4) pre.ksw[t4] = kscale(ksb, KB0 + t4);
+        for (int t4 = 0; t4 < NA; ++t4) pre.ksw[t4] = KSDMA ? kscale_raw(ksb, KB0 + t4) : kscale(ksb, KB0 + t4);
     }
 
     // NA < 4: the wave's keys are the tile's 32-key blocks KB0 .. KB0 + NA - 1 (NA = 2: one 64-key half; 2 NA QK and
@@ -1136,7 +1139,10 @@ __device__ __forceinline__ void epilogue(const Prm& p, const Wave<NT>& w, uint32
         const float hl = h2f(w.bw) + h2f(w.bw >> 16);
         const size_t prow = (size_t)split * p.rows_total + ((size_t)bidx * p.S + row) * p.H + head;
         // an empty range (l = 0) gets -1e30: the combine gives it weight 0
-        store4_system(p.lse + prow, l > 0.0f ? __builtin_amdgcn_logf(l_total) + (hl * 2048.0f) * -1.0f : -1.0e30f);
+        // a write-back store: the H words of a row are consecutive, and the KV split's one-query-tile grids put the
+        // blocks of those H heads on one XCD (kvsplit_kernel), so its L2 merges them into whole lines (written through,
+        // each 4-byte word cost a 32-byte memory write)
+        *(GLOBAL_AS float*)(p.lse + prow) = l > 0.0f ? __builtin_amdgcn_logf(l_total) + (hl * 2048.0f) * -1.0f : -1.0e30f;
     }
 }
 
@@ -1210,6 +1216,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     constexpr int NA = HV ? 2 : 4;              // 32-key accumulators per tile and wave
     constexpr int KB0 = HV && GB ? 2 : 0;       // the first of them
     const Recipe rc = recipe(LUT);
+    constexpr bool kKsDma = FMHA_KSDMA != 0;   // K-scale words copied straight into LDS (shifted on read)
     const uint32_t tblk = ((bidx * p.splits + split) * p.H + head) * ((p.S + 255u) / 256u) + qtile;
     (void)tblk;
     FMHA_MARK(p, tblk, 0);
@@ -1253,6 +1260,19 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
         // Every prologue load goes out at once (Q and its scales were issued by init): the K-scale words of tiles 0..2,
         // then the copies. One memory round trip to the first barrier (the stores of the words wait for their loads).
         st.init_dma();
+        if (kKsDma) {
+            st.dma_ks(key_of(0), true, 0);
+            st.dma_ks(key_of(1), ntiles > 1, 1);
+            st.dma(key_of(0), true, 0, key_of(0), true, 0);                 // K 0, V 0
+            st.dma(key_of(1), ntiles > 1, 1, key_of(1), false, 3);          // K 1 (V slot 3 gets zeros, nothing reads it yet)
+            if (VS) st.dma_vs(key_of(0), true, 0);                          // V scales of tile 0
+            st.dma(key_of(2), ntiles > 2, 2, key_of(1), ntiles > 1, 1);     // K 2, V 1
+            if (VS) st.dma_vs(key_of(1), ntiles > 1, 1);                    // V scales of tile 1
+            st.dma_ks(key_of(2), ntiles > 2, 2);
+            w.commit_q();
+            // everything but the copies of K 2, V 1 and the K-scale words of tile 2 (which barrier 0 waits for)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * Stager<NT>::kN + 1 + (VS ? 1 : 0)) : "memory");
+        } else {
         const uint32_t ks0 = st.ks_word(key_of(0), true);
         const uint32_t ks1 = st.ks_word(key_of(1), ntiles > 1);
         st.load_ks(key_of(2), ntiles > 2);                              // stored by V(0)
@@ -1268,20 +1288,22 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
         w.commit_q();
         // everything but the copies of K 2 and V 1 (which barrier 0 waits for)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * Stager<NT>::kN + (VS ? 1 : 0)) : "memory");
+        }
         FMHA_MARK(p, tblk, 2);
         block_barrier();
         FMHA_MARK(p, tblk, 3);
-        w.template qk_all<KB0>(0, s);
+        w.template qk_all<KB0, NA, kKsDma>(0, s);
         float mrow = row_max(s);   // unmasked row max of the tile the next VALU phase decides on
         {
             typename Wave<NT>::Ring ring;
             typename Wave<NT>::QkPre pre;
             auto v_phase = [&](uint32_t t, uint32_t (&pw)[NA][4], bool last) {
                 FMHA_SETPRIO(0);
-                st.store_ks(slot_of(t + 2));
+                if (!kKsDma) st.store_ks(slot_of(t + 2));
                 st.dma(key_of(t + 3), t + 3 < ntiles, slot_of(t + 3), key_of(t + 2), t + 2 < ntiles, slot_of(t + 2));
                 if (VS) st.dma_vs(key_of(t + 2), t + 2 < ntiles, slot_of(t + 2));
-                st.load_ks(key_of(t + 3), t + 3 < ntiles);
+                if (kKsDma) st.dma_ks(key_of(t + 3), t + 3 < ntiles, slot_of(t + 3));
+                else st.load_ks(key_of(t + 3), t + 3 < ntiles);
                 if (SC) w.scale_s(s, mrow);   // the in-kernel softmax scale (an instantiation of its own)
                 if (w.needs_mask(key_of(t))) {
                     w.template apply_mask<KB0>(s, key_of(t));
@@ -1292,7 +1314,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
                 for (int t4 = 0; t4 < NA; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
                 if (!last) {
                     s[NA - 1] = splat16(w.bias);
-                    w.template qk_prefetch<NA, KB0>(slot_of(t + 1), ring, pre);
+                    w.template qk_prefetch<NA, KB0, kKsDma>(slot_of(t + 1), ring, pre);
                 }
                 FMHA_LMARK(p, tblk, t, 0);
                 // A: the copies of the previous VALU phase have landed; this phase's and the prefetched reads stay in flight
@@ -1538,7 +1560,19 @@ __device__ __forceinline__ void kvsplit_kernel(uint32_t smem_base) {
     p.vs32 = (split_field & FMHA_KVS_V_SEQ32) ? (const uint8_t*)p.vd : nullptr;   // 0x280 is not `flags` here
     p.rows_total = ka<uint32_t>(offsetof(fmha_mxfp8_kvsplit_args, kvs_rows_total));
     uint32_t qt, head, z;
-    block_coords(p.S, p.H, 256u, qt, head, z);
+    const uint32_t gz = p.rows_total / (p.S * p.H) * p.splits;   // B x splits
+    if ((p.S + 255u) / 256u == 1u && (gz & 7u) == 0u) {
+        // One query tile per (batch, head, split): no two blocks share K/V rows, so the XCD placement serves the LSE
+        // words instead. Block L of the (H, gz) grid goes to XCD L mod 8; L -> z = (L mod 8) + 8 ((L / 8) / H),
+        // head = (L / 8) mod H puts the H heads of one split on one XCD, and the H consecutive LSE words of a row
+        // (row index (b S + s) H + h) meet in one L2, which writes them back as whole lines.
+        const uint32_t L = blockIdx.y + p.H * blockIdx.z, j = L >> 3;
+        qt = 0;
+        head = __builtin_amdgcn_readfirstlane(j % p.H);
+        z = __builtin_amdgcn_readfirstlane((L & 7u) + 8u * (j / p.H));
+    } else {
+        block_coords(p.S, p.H, 256u, qt, head, z);
+    }
     // components.rs:20-30 / 58-74: z = batch * splits + split; split s owns tiles [s tps, min(ntiles, (s+1) tps))
     const uint32_t bidx = z / p.splits, split = z % p.splits;
     const uint32_t ntiles = (p.SK + 127u) / 128u;
@@ -1653,21 +1687,29 @@ extern "C" __global__ void __launch_bounds__(512, 1) fmha_fwd_hd128_mxfp8_v3_t12
 }
 
 // epilogue.rs:89-167 / io.rs:164-185: thread t -> 8 consecutive outputs of row t >> 4 (tail threads redo the last group)
-extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvsplit_combine8h(fmha_mxfp8_combine_args a_) {
-    (void)a_;
-    const uint32_t rows = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, rows_total));
-    const uint32_t split_field = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, splits));
+// The combines take the 36-byte layout (fmha_mxfp8_combine_args: three pointers, then rows_total, d and the split
+// field at 0x18, 0x1C, 0x20) as scalar parameters, which lay out the same bytes: as scalars the nine dwords are preloaded
+// into SGPRs by the hardware at wave launch (the build's -amdgpu-kernarg-preload-count), so the kernel starts on its loads
+// without a memory round trip for its arguments. (An aggregate parameter is not preloaded.)
+#define FMHA_COMBINE_PARAMS \
+    const uint8_t* ohat, const float* lse, uint8_t* out, uint32_t rows, uint32_t d, uint32_t split_field
+static_assert(offsetof(fmha_mxfp8_combine_args, ptr_ohat) == 0x00 && offsetof(fmha_mxfp8_combine_args, ptr_lse) == 0x08 &&
+                  offsetof(fmha_mxfp8_combine_args, ptr_out) == 0x10 && offsetof(fmha_mxfp8_combine_args, rows_total) == 0x18 &&
+                  offsetof(fmha_mxfp8_combine_args, d) == 0x1C && offsetof(fmha_mxfp8_combine_args, splits) == 0x20 &&
+                  sizeof(fmha_mxfp8_combine_args) == 36,
+              "the combine kernels' scalar parameters follow the packed layout");
+
+extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvsplit_combine8h(FMHA_COMBINE_PARAMS) {
+    (void)d;
     const uint32_t groups = rows << 4;
     uint32_t t = blockIdx.x * 256u + threadIdx.x;
     t = t < groups ? t : groups - 1u;
-    const float* lse = (const float*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_lse));
-    const uint8_t* ohat = (const uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_ohat));
     const uint32_t splits = split_field & 0xffffu;
     MergeState st;
     merge_init(st);
     if (split_field & FMHA_KVS_F32_PARTIALS) merge_splits<true>(lse, ohat, rows, 0u, splits, t, st);
     else merge_splits<false>(lse, ohat, rows, 0u, splits, t, st);
-    store16_system((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u, merge_finish(st));
+    store16_system(out + (size_t)t * 16u, merge_finish(st));
 }
 
 // Extension (no counterpart in the reference): the same merge for many splits, with the splits spread over the block's
@@ -1675,18 +1717,14 @@ extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvspli
 // the last group); wave p merges the p-th quarter of the splits (ceil(splits / 4) each, in order), and wave 0 merges
 // the quarters in order through LDS. With the reference kernel's layout one thread walks every split of its group in
 // turn: at 32 splits that is 4 dependent rounds of loads on 64 groups per block (13.7 us at 1024 rows on MI355X).
-extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvsplit_combine_wide(fmha_mxfp8_combine_args a_) {
-    (void)a_;
+extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvsplit_combine_wide(FMHA_COMBINE_PARAMS) {
+    (void)d;
     __shared__ float part[3][10][64];
-    const uint32_t rows = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, rows_total));
-    const uint32_t split_field = ka<uint32_t>(offsetof(fmha_mxfp8_combine_args, splits));
     const uint32_t splits = split_field & 0xffffu;
     const uint32_t groups = rows << 4;
     const uint32_t lane = threadIdx.x & 63u, p = threadIdx.x >> 6;
     uint32_t t = blockIdx.x * 64u + lane;
     t = t < groups ? t : groups - 1u;
-    const float* lse = (const float*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_lse));
-    const uint8_t* ohat = (const uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_ohat));
     const uint32_t per = (splits + 3u) >> 2;
     const uint32_t lo = min(p * per, splits), hi = min(lo + per, splits);
     MergeState st;
@@ -1714,5 +1752,5 @@ extern "C" __global__ void __launch_bounds__(256) fmha_fwd_hd128_mxfp8_v3_kvspli
         for (int i = 0; i < 8; ++i) o.acc[i] = part[q][2 + i][lane];
         merge_states(st, o);
     }
-    store16_system((uint8_t*)ka<uint64_t>(offsetof(fmha_mxfp8_combine_args, ptr_out)) + (size_t)t * 16u, merge_finish(st));
+    store16_system(out + (size_t)t * 16u, merge_finish(st));
 }

@@ -9,8 +9,8 @@
    with no more bad elements than the reference kernel on the same path, and its parity rule, mean |err| <= 1.10 x the
    reference kernel's (run_ref.sh:65-76); on uniform data, element-wise outside the rows whose winner the MFMA's
    rounding decides (test_run_ref_gate). The reference kernel is not runnable here; its numbers are the bit-level emulation of
-   its recipe (oracle.emulate), which reproduces the harness's published figures (docs/vendor-spec.md:1117-1118: at 64
-   rows the three lcg shapes with bad = 1 / 4 / 5, the same counts the emulation gives).
+   its recipe (oracle.emulate), which reproduces the reference's 25 published per-shape accuracies (docs/perf-matrix.md,
+   tests/test_gpu_published.py).
 2. determinism.sh:56-69: 5 shapes x 3 launches, bit-identical outputs, on every path (plus the KV split at config 5 and
    the headline shape, where the copy schedule's old race showed as run-to-run variation).
 3. ref_host.cpp:602-639: the KV split against the full-sequence _vs128 kernel on the same inputs. The gate's fixed bar
