@@ -51,9 +51,6 @@ namespace {
 #ifndef FMHA_PREFETCH
 #define FMHA_PREFETCH 2
 #endif
-#ifndef FMHA_KSDMA
-#define FMHA_KSDMA 0
-#endif
 
 constexpr int kD = 128;
 constexpr int kTile = 128;                    // keys per KV tile
@@ -750,7 +747,7 @@ struct Wave {
         v8i qf0;
         uint32_t ksw[4];
     };
-    template <int NA = 4, int KB0 = 0, bool KSDMA = false>
+    template <int NA = 4, int KB0 = 0>
     __device__ __forceinline__ void qk_prefetch(uint32_t kslot, Ring& ring, QkPre& pre) const {
         static_assert(DEPTH <= 2 * NA, "the prefetched operands are K fragments");
         const uint32_t kb = slot_base(lds, kLdsK, kslot, kTileBytes);
@@ -759,7 +756,7 @@ struct Wave {
         for (int i = 0; i < DEPTH; ++i) ring[i] = frag(kb, i / NA, 4096u * (uint32_t)(KB0 + i % NA));
         pre.qf0 = qfrag(0);
 #pragma unroll
-        for (int t4 = 0; t4 < NA; ++t4) pre.ksw[t4] = KSDMA ? kscale_raw(ksb, KB0 + t4) : kscale(ksb, KB0 + t4);
+        for (int t4 = 0; t4 < NA; ++t4) pre.ksw[t4] = kscale(ksb, KB0 + t4);
     }
 
     // NA < 4: the wave's keys are the tile's 32-key blocks KB0 .. KB0 + NA - 1 (NA = 2: one 64-key half; 2 NA QK and
@@ -1216,7 +1213,6 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     constexpr int NA = HV ? 2 : 4;              // 32-key accumulators per tile and wave
     constexpr int KB0 = HV && GB ? 2 : 0;       // the first of them
     const Recipe rc = recipe(LUT);
-    constexpr bool kKsDma = FMHA_KSDMA != 0;   // K-scale words copied straight into LDS (shifted on read)
     const uint32_t tblk = ((bidx * p.splits + split) * p.H + head) * ((p.S + 255u) / 256u) + qtile;
     (void)tblk;
     FMHA_MARK(p, tblk, 0);
@@ -1260,19 +1256,6 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
         // Every prologue load goes out at once (Q and its scales were issued by init): the K-scale words of tiles 0..2,
         // then the copies. One memory round trip to the first barrier (the stores of the words wait for their loads).
         st.init_dma();
-        if (kKsDma) {
-            st.dma_ks(key_of(0), true, 0);
-            st.dma_ks(key_of(1), ntiles > 1, 1);
-            st.dma(key_of(0), true, 0, key_of(0), true, 0);                 // K 0, V 0
-            st.dma(key_of(1), ntiles > 1, 1, key_of(1), false, 3);          // K 1 (V slot 3 gets zeros, nothing reads it yet)
-            if (VS) st.dma_vs(key_of(0), true, 0);                          // V scales of tile 0
-            st.dma(key_of(2), ntiles > 2, 2, key_of(1), ntiles > 1, 1);     // K 2, V 1
-            if (VS) st.dma_vs(key_of(1), ntiles > 1, 1);                    // V scales of tile 1
-            st.dma_ks(key_of(2), ntiles > 2, 2);
-            w.commit_q();
-            // everything but the copies of K 2, V 1 and the K-scale words of tile 2 (which barrier 0 waits for)
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * Stager<NT>::kN + 1 + (VS ? 1 : 0)) : "memory");
-        } else {
         const uint32_t ks0 = st.ks_word(key_of(0), true);
         const uint32_t ks1 = st.ks_word(key_of(1), ntiles > 1);
         st.load_ks(key_of(2), ntiles > 2);                              // stored by V(0)
@@ -1288,22 +1271,20 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
         w.commit_q();
         // everything but the copies of K 2 and V 1 (which barrier 0 waits for)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * Stager<NT>::kN + (VS ? 1 : 0)) : "memory");
-        }
         FMHA_MARK(p, tblk, 2);
         block_barrier();
         FMHA_MARK(p, tblk, 3);
-        w.template qk_all<KB0, NA, kKsDma>(0, s);
+        w.template qk_all<KB0>(0, s);
         float mrow = row_max(s);   // unmasked row max of the tile the next VALU phase decides on
         {
             typename Wave<NT>::Ring ring;
             typename Wave<NT>::QkPre pre;
             auto v_phase = [&](uint32_t t, uint32_t (&pw)[NA][4], bool last) {
                 FMHA_SETPRIO(0);
-                if (!kKsDma) st.store_ks(slot_of(t + 2));
+                st.store_ks(slot_of(t + 2));
                 st.dma(key_of(t + 3), t + 3 < ntiles, slot_of(t + 3), key_of(t + 2), t + 2 < ntiles, slot_of(t + 2));
                 if (VS) st.dma_vs(key_of(t + 2), t + 2 < ntiles, slot_of(t + 2));
-                if (kKsDma) st.dma_ks(key_of(t + 3), t + 3 < ntiles, slot_of(t + 3));
-                else st.load_ks(key_of(t + 3), t + 3 < ntiles);
+                st.load_ks(key_of(t + 3), t + 3 < ntiles);
                 if (SC) w.scale_s(s, mrow);   // the in-kernel softmax scale (an instantiation of its own)
                 if (w.needs_mask(key_of(t))) {
                     w.template apply_mask<KB0>(s, key_of(t));
@@ -1314,7 +1295,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
                 for (int t4 = 0; t4 < NA; ++t4) convert_p<LUT>(rc, s[t4], pw[t4]);
                 if (!last) {
                     s[NA - 1] = splat16(w.bias);
-                    w.template qk_prefetch<NA, KB0, kKsDma>(slot_of(t + 1), ring, pre);
+                    w.template qk_prefetch<NA, KB0>(slot_of(t + 1), ring, pre);
                 }
                 FMHA_LMARK(p, tblk, t, 0);
                 // A: the copies of the previous VALU phase have landed; this phase's and the prefetched reads stay in flight
