@@ -409,7 +409,7 @@ def kernel_launcher(lib, q, k, v, qs, ks, vs, out, lse, used, B, H, HK, S, SK, c
     a.ptr_lse = lse.data_ptr() if lse is not None else None
     sz = lib.BufferSizes(_cap(q), _cap(k), _cap(v), _cap(out), _cap(qs), _cap(ks), _cap(vs), 0, 0)
     st = stream.cuda_stream
-    path, nsplit = used
+    path = used[0]
     kernel = "fmha_fwd_hd128_mxfp8_v3_" + path
     if path in ("vs128", "t128"):
         split_tiles = lib.uses_split_tiles(path, B, H, S, SK, causal)
@@ -430,19 +430,30 @@ def kernel_launcher(lib, q, k, v, qs, ks, vs, out, lse, used, B, H, HK, S, SK, c
         if split_tiles:
             kernel = "fmha_fwd_hd128_mxfp8_v3_t128_split_tiles"
     else:
+        # the split kernel as the entry runs it: the partials that ran (the KV fill's), over the entry's workspace slots
+        # in turn (one slot would have each launch write over the lines the previous one wrote)
+        nsplit = used.partials
         rows_total = B * S * H
-        ws = torch.empty(lib.workspace_bytes(B, H, S, nsplit), dtype=torch.uint8, device=q.device)
-        ka = lib.KvsplitArgs()
-        ctypes.memmove(ctypes.addressof(ka), ctypes.addressof(a), 0x270)
-        ka.ptr_ohat = ws.data_ptr()
-        ka.ptr_lse = ws.data_ptr() + nsplit * rows_total * 512
-        ka.kvs_splits, ka.kvs_rows_total = nsplit, rows_total
+        need = lib.workspace_bytes(B, H, S, nsplit)
+        stride = (need + 255) // 256 * 256
+        ws = torch.empty(lib.WORKSPACE_SLOTS * stride, dtype=torch.uint8, device=q.device)
+        kas = []
+        for slot in range(lib.WORKSPACE_SLOTS):
+            ka = lib.KvsplitArgs()
+            ctypes.memmove(ctypes.addressof(ka), ctypes.addressof(a), 0x270)
+            ka.ptr_ohat = ws.data_ptr() + slot * stride
+            ka.ptr_lse = ka.ptr_ohat + nsplit * rows_total * 512
+            ka.kvs_splits, ka.kvs_rows_total = nsplit, rows_total
+            kas.append(ka)
         grid = (math.ceil(S / 256), H, B * nsplit)
         sz.ptr_ohat, sz.ptr_lse = nsplit * rows_total * 512, nsplit * rows_total * 4
-        rc, msg = lib.validate("kvsplit", ka, sz, grid, B=B, HK=HK, KL=0)
+        rc, msg = lib.validate("kvsplit", kas[0], sz, grid, B=B, HK=HK, KL=0)
         assert rc == 0, msg
-        # (the closure holds the workspace tensor, so it lives as long as the launcher)
-        launch = lambda ws=ws: lib.raw.fmha_mxfp8_launch_kvsplit(ctypes.byref(ka), *grid, st)
+        turn = [0]
+
+        def launch(ws=ws):   # (the default argument keeps the workspace tensor alive with the launcher)
+            turn[0] += 1
+            return lib.raw.fmha_mxfp8_launch_kvsplit(ctypes.byref(kas[turn[0] % len(kas)]), *grid, st)
     for _ in range(20):
         assert launch() == 0
     torch.cuda.synchronize()
