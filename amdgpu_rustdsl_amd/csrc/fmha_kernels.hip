@@ -1541,7 +1541,7 @@ __device__ __forceinline__ void kvsplit_kernel(uint32_t smem_base) {
     p.vs32 = (split_field & FMHA_KVS_V_SEQ32) ? (const uint8_t*)p.vd : nullptr;   // 0x280 is not `flags` here
     p.rows_total = ka<uint32_t>(offsetof(fmha_mxfp8_kvsplit_args, kvs_rows_total));
     uint32_t qt, head, z;
-    const uint32_t gz = p.rows_total / (p.S * p.H) * p.splits;   // B x splits
+    const uint32_t gz = p.rows_total / (p.S * p.H) * p.splits;   // B x splits (rows_total = B S H: validate's rule)
     if ((p.S + 255u) / 256u == 1u && (gz & 7u) == 0u) {
         // One query tile per (batch, head, split): no two blocks share K/V rows, so the XCD placement serves the LSE
         // words instead. Block L of the (H, gz) grid goes to XCD L mod 8; L -> z = (L mod 8) + 8 ((L / 8) / H),
