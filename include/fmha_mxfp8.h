@@ -310,8 +310,9 @@ int fmha_fwd_hd128_mxfp8_auto(const fmha_mxfp8_params* p, void* workspace, size_
  * that forbid hipMalloc). The KV split's workspace is a device array of FMHA_NOALLOC_SCRATCH_BYTES inside the library
  * instead of a caller's buffer, one per device, held until the process ends; a shape whose split needs more is
  * rejected with FMHA_ERR_WORKSPACE. The largest workspace the auto dispatch asks for is 2 splits x 32768 rows x 516 B
- * (blocks256 <= 128 bounds B S H to 32768): exactly this size; the KV fill and the workspace slots use as much of it
- * as it holds. The first call on a device looks the array up and loads
+ * (blocks256 <= 128 bounds B S H to 32768): exactly this size; the KV fill and the workspace slots (taken in turn
+ * through p->ws_turn when the caller passes one, else slot 0) use as much of it as it holds. The first call on a
+ * device looks the array up and loads
  * the code objects (fmha_mxfp8_init); later calls call no allocating routine and no hipMalloc/hipFree. Calls on one
  * device share its array: calls that overlap on one device (unordered streams) race. Otherwise identical to
  * fmha_fwd_hd128_mxfp8_auto (same params, rules, errors and kernels). */
