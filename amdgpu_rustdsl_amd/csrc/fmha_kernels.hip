@@ -1270,9 +1270,9 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
         // -2.4 %, cfg3 -0.6 %).
         st.store_ks_word(ks0, 0);
         st.store_ks_word(ks1, 1);
+        w.commit_q();   // (its wait for the Q scale word likewise comes before the copies of K 2 and V 1)
         st.dma(key_of(2), ntiles > 2, 2, key_of(1), ntiles > 1, 1);     // K 2, V 1
         if (VS) st.dma_vs(key_of(1), ntiles > 1, 1);                    // V scales of tile 1
-        w.commit_q();
         // everything but the copies of K 2 and V 1 (which barrier 0 waits for)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * Stager<NT>::kN + (VS ? 1 : 0)) : "memory");
         FMHA_MARK(p, tblk, 2);
@@ -1402,8 +1402,10 @@ __device__ __forceinline__ void attend_single_wave(const Prm& p, uint32_t lds, u
         };
         copy_tile(0);
         copy_tile(1);
-        copy_tile(2);
+        // the compiler's wait for the Q scale word (it does not count the copies' inline assembly) comes before tile
+        // 2's copies, so that it does not hold the first barrier for them (cfg1 -1.5 %)
         w.commit_q();
+        copy_tile(2);
         // VMEM operations per tile: the K and V copies, the K-scale copy and (extension) the V-scale copy
         constexpr int kOps = 2 * Stager<NT>::kN + 1 + (VS ? 1 : 0);
         FMHA_MARK(p, tblk, 2);
