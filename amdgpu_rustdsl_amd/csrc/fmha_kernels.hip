@@ -272,8 +272,24 @@ __device__ inline void store4_system(void* ptr, float x) {
 __device__ inline v2i lds_read_tr8(uint32_t off) { return __builtin_amdgcn_ds_read_tr8_b64_v2i32((LDS_AS v2i*)(uintptr_t)off); }
 
 typedef float v8f __attribute__((ext_vector_type(8)));
-__device__ inline v8f splat8(float x) { return (v8f){x, x, x, x, x, x, x, x}; }
-__device__ inline v16f splat16(float x) { return (v16f){x, x, x, x, x, x, x, x, x, x, x, x, x, x, x, x}; }
+// Splats in 64-bit halves: one move makes the pair (x, x), then v_mov_b64 copies the pair; each copy goes through an
+// empty asm, so that the compiler keeps it a 64-bit copy instead of splitting it into 32-bit moves (the bias seed of S
+// and the ones operand: 10 fewer VALU instructions per tile and wave, cfg2 and cfg3 -0.3 %).
+typedef unsigned long long v4u64 __attribute__((ext_vector_type(4)));
+typedef unsigned long long v8u64 __attribute__((ext_vector_type(8)));
+__device__ inline unsigned long long pair2(float x) {
+    const unsigned long long u = __builtin_bit_cast(uint32_t, x);
+    return u | (u << 32);
+}
+__device__ inline unsigned long long opq(unsigned long long q) { asm volatile("" : "+v"(q)); return q; }
+__device__ inline v8f splat8(float x) {
+    const unsigned long long q = pair2(x);
+    return __builtin_bit_cast(v8f, (v4u64){q, opq(q), opq(q), opq(q)});
+}
+__device__ inline v16f splat16(float x) {
+    const unsigned long long q = pair2(x);
+    return __builtin_bit_cast(v16f, (v8u64){q, opq(q), opq(q), opq(q), opq(q), opq(q), opq(q), opq(q)});
+}
 __device__ inline v8i cat8(v4i a, v4i b) { return (v8i){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}; }
 
 __device__ inline const uint8_t* uniform_ptr(const uint8_t* p) {
