@@ -1229,16 +1229,16 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     constexpr int NA = HV ? 2 : 4;              // 32-key accumulators per tile and wave
     constexpr int KB0 = HV && GB ? 2 : 0;       // the first of them
     const Recipe rc = recipe(LUT);
-    const uint32_t tblk = ((bidx * p.splits + split) * p.H + head) * ((p.S + 255u) / 256u) + qtile;
+    // rows per block: 256, or 128 for the full-sequence split-tile kernel (the KV split's split-tile blocks keep the
+    // 256-row grid and use their first 128 rows)
+    constexpr uint32_t RB = HV && !SPLIT ? 128u : 256u;
+    const uint32_t tblk = ((bidx * p.splits + split) * p.H + head) * ((p.S + RB - 1u) / RB) + qtile;   // trace slot
     (void)tblk;
     FMHA_MARK(p, tblk, 0);
 #ifdef FMHA_TRACE
     if (p.trace && (threadIdx.x & 63u) == 0u) p.trace[((size_t)tblk * 8u + (threadIdx.x >> 6)) * 8u + 7u] = p.t_entry;
 #endif
     Wave<NT> w;
-    // rows per block: 256, or 128 for the full-sequence split-tile kernel (the KV split's split-tile blocks keep the
-    // 256-row grid and use their first 128 rows)
-    constexpr uint32_t RB = HV && !SPLIT ? 128u : 256u;
     w.init(p, lds, qtile, head, bidx, key_hi, HV ? wave_id() & 3u : wave_id(), RB);
     FMHA_MARK(p, tblk, 1);
     const uint32_t kvh = head / p.gqa;
@@ -1360,6 +1360,7 @@ __device__ __forceinline__ void attend_pingpong_group(const Prm& p, uint32_t lds
     } else {
         // HV: each group finishes half of every row's dims (A 0..63, B 64..127); the merge's barriers retired the ring
         merge_halves<GB>(w, lds);
+        FMHA_MARK(p, tblk, 6);
         epilogue<SPLIT, NT, false, GB ? 2 : 1>(p, w, head, bidx, split, rc, false);
     }
     FMHA_MARK(p, tblk, 5);
