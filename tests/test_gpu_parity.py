@@ -524,3 +524,59 @@ def test_parity_128row_single_wave(gpu, case):
     assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
     assert cmp["max_abs"] <= 0.05, cmp
     np.testing.assert_array_equal(gpu_util.run_direct(inp, gpu, path), out)
+
+
+def _random_cases(n=16, seed=20261202):
+    """Seeded random shapes for the one-call entry's dispatch (every path it can pick, ragged S and SK, GQA, causal):
+    sizes at which the oracle checks them in seconds."""
+    rs = np.random.RandomState(seed)
+    cases = []
+    for i in range(n):
+        H = int(rs.choice([1, 2, 4, 8]))
+        HK = int(rs.choice([d for d in (1, 2, 4, 8) if d <= H and H % d == 0]))
+        B = int(rs.randint(1, 4)) if H <= 4 else int(rs.randint(1, 3))
+        S = int(rs.randint(1, 200)) if rs.rand() < 0.4 else int(rs.randint(200, 1300))
+        SK = int(rs.randint(1, 300)) if rs.rand() < 0.3 else int(rs.randint(300, 2600))
+        causal = bool(rs.rand() < 0.3)
+        cases.append((f"rand{i}_B{B}H{H}HK{HK}_S{S}_SK{SK}" + ("_causal" if causal else ""), B, H, HK, S, SK, causal))
+    # grids of more than 128 256-row blocks, where the dispatch picks the 256-row vs128 kernel
+    for i in range(4):
+        B = int(rs.randint(4, 9))
+        HK = int(rs.choice([2, 4, 8]))
+        S = int(rs.randint(1100, 2100))
+        SK = int(rs.randint(200, 1300))
+        causal = i % 2 == 1
+        cases.append((f"randL{i}_B{B}H8HK{HK}_S{S}_SK{SK}" + ("_causal" if causal else ""), B, 8, HK, S, SK, causal))
+    return cases
+
+
+RANDOM_CASES = _random_cases()
+
+
+@pytest.mark.parametrize("case", RANDOM_CASES, ids=[c[0] for c in RANDOM_CASES])
+def test_parity_random_shapes(gpu, case):
+    """The fixed cases' bars (test_parity, test_parity_causal) on seeded random shapes through the automatic
+    dispatch."""
+    name, B, H, HK, S, SK, causal = case
+    print(f"[case] {name}", flush=True)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
+    out, used, _ = gpu_util.run(inp, gpu)
+    rows = S if S <= 128 else oracle.first_and_last(S, ROWS)
+    used_splits = used.partials if used[0] == "kvsplit" else 0
+    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0], ref_splits=gpu_util.chunks(inp))
+    stats = oracle.check_fp64(inp, out, rows=rows)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
+    print(f"[case] {name} path={used} partials={used.partials} ours={stats} emulated-reference={ref_stats} "
+          f"vs-emulation={cmp}", flush=True)
+    assert not np.isnan(oracle.bf16_to_f32(out)).any(), "unwritten / NaN outputs"
+    assert stats["bad"] <= ref_stats["bad"]
+    assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
+    assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
+    if causal:
+        fig, viol = gpu_util.causal_bar(inp, out, emu, rows)
+        assert not viol, (viol, fig)
+        if S > SK:
+            o = oracle.bf16_to_f32(out).reshape(B, S, H, 128)
+            assert (o[:, : S - SK] == 0).all()
+    else:
+        assert cmp["max_abs"] <= 0.05, cmp
