@@ -115,14 +115,30 @@ def run_direct(inp, device, kernel):
 
 
 def _dequant(inp):
-    """float64 dequantised Q [B,S,H,128], K and V [B,SK,HK,128] (V with its descale; the per-tensor descale only)."""
+    """float64 dequantised Q [B,S,H,128], K and V [B,SK,HK,128], V with its scales as the oracle's float64 check takes
+    them (mxfp8_oracle.c v_block_scale / v_tensor_descale): one E8M0 per 32 keys and column under per-32-key V scales,
+    else the per-tensor descale."""
     dec = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy().astype(np.float64)
     dec[[0x7F, 0xFF]] = 0.0
     B, H, HK, S, SK = inp.B, inp.H, inp.HK, inp.S, inp.SK
     q = dec[inp.q].reshape(B, S, H, 4, 32) * 2.0 ** (inp.qs[: B * S * H * 4].reshape(B, S, H, 4, 1).astype(np.float64) - 127)
     k = dec[inp.k].reshape(B, SK, HK, 4, 32) * 2.0 ** (inp.ks[: B * SK * HK * 4].reshape(B, SK, HK, 4, 1).astype(np.float64) - 127)
-    v = dec[inp.v].reshape(B, SK, HK, D) * float(inp.vdescale)
+    v = dec[inp.v[: B * SK * HK * D]].reshape(B, SK, HK, D)
+    if inp.vs32 is not None:
+        nb = (SK + 31) // 32
+        e = np.asarray(inp.vs32, dtype=np.uint8)[: B * nb * HK * D].reshape(B, nb, HK, D).astype(np.float64)
+        v = v * np.repeat(2.0 ** (e - 127), 32, axis=1)[:, :SK]
+    else:
+        v = v * float(inp.vdescale)
     return q.reshape(B, S, H, D), k.reshape(B, SK, HK, D), v
+
+
+def score_scale(inp):
+    """The base-2 score multiplier: 1, or under the in-kernel softmax scale c = f32(scale) * f32(log2 e) in f32
+    (mxfp8_oracle.c qk_scaling_of)."""
+    if not inp.qk_scale > 0:
+        return 1.0
+    return float(np.float32(inp.qk_scale) * np.float32(1.4426950408889634))
 
 
 def fp64_rows(inp, rows):
@@ -140,8 +156,8 @@ def fp64_rows(inp, rows):
     for b in range(B):
         for h in range(H):
             qs, ks = q[b, sel, h], k[b, :, h // g]
-            s = qs @ ks.T
-            m = np.abs(qs) @ np.abs(ks).T
+            s = (qs @ ks.T) * score_scale(inp)
+            m = (np.abs(qs) @ np.abs(ks).T) * score_scale(inp)
             order = np.argsort(-s, axis=1)
             top = np.take_along_axis(s, order[:, :2], 1) if s.shape[1] > 1 else np.concatenate([s, s - np.inf], 1)
             gap[b, :, h] = top[:, 0] - top[:, 1]
@@ -167,7 +183,7 @@ def causal_rows(inp, rows):
     flip = np.zeros((B, sel.size, H, D))
     for b in range(B):
         for h in range(H):
-            s = q[b, sel, h] @ k[b, :, h // g].T
+            s = (q[b, sel, h] @ k[b, :, h // g].T) * score_scale(inp)
             s[np.arange(SK)[None, :] >= vis[:, None]] = -np.inf
             live = vis > 0
             s = s[live]

@@ -580,3 +580,68 @@ def test_parity_random_shapes(gpu, case):
             assert (o[:, : S - SK] == 0).all()
     else:
         assert cmp["max_abs"] <= 0.05, cmp
+
+
+def _random_ext_cases(n=16, seed=77):
+    """Seeded random combinations of the extensions (per-32-key V scales, the in-kernel softmax scale, f32 partials,
+    causal) with a forced path, on random shapes."""
+    rs = np.random.RandomState(seed)
+    cases = []
+    for i in range(n):
+        H = int(rs.choice([1, 2, 4, 8]))
+        HK = int(rs.choice([d for d in (1, 2, 4, 8) if d <= H and H % d == 0]))
+        B = int(rs.randint(1, 3))
+        S = int(rs.randint(1, 150)) if rs.rand() < 0.3 else int(rs.randint(150, 1100))
+        SK = int(rs.randint(1, 400)) if rs.rand() < 0.3 else int(rs.randint(400, 2500))
+        path = str(rs.choice(["vs128", "t128", "kvsplit"]))
+        causal = path != "kvsplit" and rs.rand() < 0.4
+        splits = int(rs.choice([2, 4, 8])) if path == "kvsplit" else None
+        if splits:
+            # validate (the reference's rule) refuses a split left without a key tile: the largest count that fits
+            nt = (SK + 127) // 128
+            while splits > 2 and (splits - 1) * -(-nt // splits) >= nt:
+                splits //= 2
+            if (splits - 1) * -(-nt // splits) >= nt:
+                SK = max(SK, 257)
+        opt = {"v_seq32": bool(rs.rand() < 0.5),
+               "qk_scale": float(rs.choice([0.0, 0.3, 0.7, 1.3])),
+               "partials": "fp32" if path == "kvsplit" and rs.rand() < 0.5 else "fp16"}
+        tag = "".join(["_causal" if causal else "", "_vs32" if opt["v_seq32"] else "",
+                       f"_c{opt['qk_scale']}" if opt["qk_scale"] else "", "_f32" if opt["partials"] == "fp32" else ""])
+        cases.append((f"ext{i}_{path}{splits or ''}_B{B}H{H}HK{HK}_S{S}_SK{SK}{tag}", B, H, HK, S, SK, causal, path,
+                      splits, opt))
+    return cases
+
+
+RANDOM_EXT_CASES = _random_ext_cases()
+
+
+@pytest.mark.parametrize("case", RANDOM_EXT_CASES, ids=[c[0] for c in RANDOM_EXT_CASES])
+def test_parity_random_extensions(gpu, case):
+    """The extensions' bars (test_parity_v_seq32, test_parity_qk_scale, test_parity_f32_partials, the causal bar) on
+    seeded random combinations."""
+    name, B, H, HK, S, SK, causal, path, splits, opt = case
+    print(f"[case] {name}", flush=True)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal, v_seq32=opt["v_seq32"], qk_scale=opt["qk_scale"])
+    out, used, _ = gpu_util.run(inp, gpu, path=path, splits=splits, partials=opt["partials"])
+    assert used[0] == path
+    rows = S if S <= 128 else oracle.first_and_last(S, ROWS)
+    used_splits = used.partials if used[0] == "kvsplit" else 0
+    emu, ref_stats = _emulated_bar(inp, used_splits, rows=rows, path=used[0], ref_splits=gpu_util.chunks(inp, path, splits),
+                                   f32_partials=opt["partials"] == "fp32")
+    stats = oracle.check_fp64(inp, out, rows=rows)
+    cmp = gpu_util.compare_to_emulation(out, emu, inp, rows)
+    print(f"[case] {name} path={used} partials={used.partials} ours={stats} emulated-reference={ref_stats} "
+          f"vs-emulation={cmp}", flush=True)
+    assert not np.isnan(oracle.bf16_to_f32(out)).any(), "unwritten / NaN outputs"
+    assert stats["bad"] <= ref_stats["bad"]
+    assert stats["mean_err"] <= 1.10 * ref_stats["mean_err"] + 1e-7
+    assert cmp["mean_abs"] <= 0.6 * max(ref_stats["mean_err"], 1e-6), cmp
+    if causal:
+        fig, viol = gpu_util.causal_bar(inp, out, emu, rows)
+        assert not viol, (viol, fig)
+        if S > SK:
+            o = oracle.bf16_to_f32(out).reshape(B, S, H, 128)
+            assert (o[:, : S - SK] == 0).all()
+    else:
+        assert cmp["max_abs"] <= 0.05, cmp

@@ -235,10 +235,12 @@ def _numpy_attention(inp, rows):
         v = dec[inp.v].reshape(B, SK, HK, D) * inp.vdescale
     q, k = q.reshape(B, S, H, D), k.reshape(B, SK, HK, D)
     g = H // HK
+    # the in-kernel softmax scale (extension): base-2 scores times c = f32(scale) f32(log2 e), rounded to f32
+    c = float(np.float32(inp.qk_scale) * np.float32(1.4426950408889634)) if inp.qk_scale > 0 else 1.0
     out = np.zeros((B, rows, H, D))
     for b in range(B):
         for h in range(H):
-            s = q[b, :rows, h] @ k[b, :, h // g].T * np.log(2.0)
+            s = q[b, :rows, h] @ k[b, :, h // g].T * np.log(2.0) * c
             if inp.causal:
                 i = np.arange(rows)[:, None]; t = np.arange(SK)[None, :]
                 s = np.where(t <= i + SK - S, s, -np.inf)
@@ -248,11 +250,13 @@ def _numpy_attention(inp, rows):
     return out
 
 
-@pytest.mark.parametrize("causal,v_seq32", [(False, False), (True, False), (False, True)])
-def test_check_fp64_matches_numpy(causal, v_seq32):
+@pytest.mark.parametrize("causal,v_seq32,scale", [(False, False, 0.0), (True, False, 0.0), (False, True, 0.0),
+                                                 (True, True, 0.7), (False, False, 1.3)])
+def test_check_fp64_matches_numpy(causal, v_seq32, scale):
     """ref_host.cpp:436-471 statistics (bad = |err| > 0.05 + 0.05 |ref|, mean |err|) of a given output == the same
-    statistics computed from numpy float64 attention (also with the per-32-key V scales of the extension)."""
-    inp = oracle.Inputs(2, 4, 40, 70, HK=2, causal=causal, v_seq32=v_seq32)
+    statistics computed from numpy float64 attention (also with the per-32-key V scales and the in-kernel softmax
+    scale of the extensions)."""
+    inp = oracle.Inputs(2, 4, 40, 70, HK=2, causal=causal, v_seq32=v_seq32, qk_scale=scale)
     rows = 24
     ref = _numpy_attention(inp, rows)
     rng = np.random.default_rng(1)
@@ -265,6 +269,21 @@ def test_check_fp64_matches_numpy(causal, v_seq32):
     assert got["checked"] == err.size
     assert got["bad"] == int((err > 0.05 + 0.05 * np.abs(ref)).sum())
     assert abs(got["mean_err"] - err.mean()) <= 1e-9 * max(1.0, err.mean())
+
+
+@pytest.mark.parametrize("causal,v_seq32,scale", [(True, True, 0.7), (False, False, 1.3), (True, False, 0.0)])
+def test_gpu_util_float64_matches_numpy(causal, v_seq32, scale):
+    """The GPU tests' float64 attention (tests/gpu_util.py: causal_rows under the causal bar, fp64_rows under the
+    gate bar) == numpy float64 attention, with the extensions' per-32-key V scales and in-kernel softmax scale."""
+    from tests import gpu_util
+    inp = oracle.Inputs(2, 4, 40, 70, HK=2, causal=causal, v_seq32=v_seq32, qk_scale=scale)
+    ref = _numpy_attention(inp, inp.S)
+    if causal:
+        got, vis, _ = gpu_util.causal_rows(inp, inp.S)
+        assert (vis == np.clip(np.arange(inp.S) + inp.SK - inp.S + 1, 0, inp.SK)).all()
+    else:
+        got, _, _ = gpu_util.fp64_rows(inp, inp.S)
+    np.testing.assert_allclose(got, ref, rtol=1e-9, atol=1e-12)
 
 
 @pytest.mark.parametrize("causal,v_seq32", [(False, False), (True, False), (False, True)])
