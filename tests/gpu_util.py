@@ -66,7 +66,8 @@ def compare_to_emulation(out, emu, inp, rows):
 
 
 def lse_reference(inp, rows):
-    """float64 natural-log LSE [B, H, rows] of the dequantised inputs (scores ln2 q.k, the kernels' base-2 convention)."""
+    """float64 natural-log LSE [B, H, rows] of the dequantised inputs (scores ln2 c q.k, the kernels' base-2 convention,
+    c the in-kernel softmax scale's multiplier or 1)."""
     dec = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy().astype(np.float64)
     dec[[0x7F, 0xFF]] = 0.0
     B, H, HK, S, SK = inp.B, inp.H, inp.HK, inp.S, inp.SK
@@ -77,7 +78,7 @@ def lse_reference(inp, rows):
     out = np.zeros((B, H, rows))
     for b in range(B):
         for h in range(H):
-            s = q[b, :rows, h] @ k[b, :, h // g].T * np.log(2.0)
+            s = q[b, :rows, h] @ k[b, :, h // g].T * (np.log(2.0) * score_scale(inp))
             if inp.causal:
                 i = np.arange(rows)[:, None]
                 t = np.arange(SK)[None, :]

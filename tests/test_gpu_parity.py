@@ -175,26 +175,31 @@ def test_parity_v_seq32(gpu, case):
     assert cmp["max_abs"] <= 0.05, cmp
 
 
+@pytest.mark.parametrize("scale", [0.0, 0.7], ids=["", "scale0.7"])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("shape", [(1, 4, 4, 512, 640), (4, 8, 8, 1024, 1024), (4, 8, 8, 2048, 2048)],
                          ids=["t128", "vs128_split_tiles", "vs128"])
-def test_lse_output(gpu, shape, causal):
-    """The optional natural-log LSE (kernarg 0x040): log sum_t exp(ln2 q.k_t) over the visible keys, against float64."""
+def test_lse_output(gpu, shape, causal, scale):
+    """The optional natural-log LSE (kernarg 0x040): log sum_t exp(ln2 c q.k_t) over the visible keys, against
+    float64 (c = 1, or the in-kernel softmax scale's multiplier)."""
     B, H, HK, S, SK = shape
-    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal)
+    inp = oracle.Inputs(B, H, S, SK, HK=HK, causal=causal, qk_scale=scale)
     out, used, lse_t = gpu_util.run(inp, gpu, lse=True)
     lse = lse_t.cpu().numpy()
-    ref = gpu_util.lse_reference(inp, rows=64)
-    got = lse[:, :, :64]
+    # under the mask every row: the first 64 see 1..64 keys, so the rows that see many keys come from further down
+    nrow = S if causal else 64
+    ref = gpu_util.lse_reference(inp, rows=nrow)
+    got = lse[:, :, :nrow]
     err = np.abs(got - ref)
-    print(f"[case] lse {shape} causal={causal} path={used} max_err={err.max():.3g} mean_err={err.mean():.3g}", flush=True)
+    print(f"[case] lse {shape} causal={causal} scale={scale} path={used} max_err={err.max():.3g} mean_err={err.mean():.3g}",
+          flush=True)
     assert np.isfinite(got).all()
     assert used[0] == ("t128" if S == 512 else "vs128")
     # l sums the recipe's P: an exp2 approximation (per key within a factor 1.087 of 2^x, bias removed on average) then
     # e4m3 rounding. A row with few visible keys (causal, top rows) keeps its keys' approximation error, up to
     # ln 1.087 = 0.083; over many keys it averages out to a few 1e-3.
     assert err.max() < 0.09
-    nvis = np.minimum(SK, np.arange(64) + SK - S + 1) if causal else np.full(64, SK)
+    nvis = np.minimum(SK, np.arange(nrow) + SK - S + 1) if causal else np.full(nrow, SK)
     many = nvis >= 64
     assert err[:, :, many].mean() < 4e-3
 
