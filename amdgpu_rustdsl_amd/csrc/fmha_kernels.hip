@@ -5,6 +5,8 @@
 //   fmha_fwd_hd128_mxfp8_v3_t128              128 query rows / 4 waves per block
 //   fmha_fwd_hd128_mxfp8_v3_kvsplit           256 rows per block over one KV split -> fp16 partials + base-2 LSE
 //   fmha_fwd_hd128_mxfp8_v3_kvsplit_combine8h LSE-weighted merge of the partials, 8 outputs per thread
+// and extensions with the same layouts: _t128_split_tiles (t128's grid, 8 waves splitting each tile's keys),
+// _kvsplit_combine_wide (the merge for many partials), and the _scaled kernels (the softmax scale applied in the kernel).
 //
 // Per wave: 32 query rows. S^T (keys x queries) = K Q^T on v_mfma_scale_f32_32x32x64_f8f6f4 with the E8M0
 // scales in the MFMA (K scale byte-selected per lane half, Q scale - 9 so S comes out x 2^-9), seeded with the
@@ -18,10 +20,11 @@
 //   shorter: eager rebase when thr < m, thr = 120/512, target 131/512, LUT-corrected pknorm, P scale 1;
 //   P = e4m3(bf16_bits(pknorm_u16(S')) / scale) (a Schraudolph exp2: the u16 read as bf16 is 2^(512 S' - 127)).
 //
-// K/V tiles reach a 3-slot LDS ring by direct HBM -> LDS copies (buffer_load_dwordx4 ... lds) in vs128/kvsplit and
-// through registers in t128; 16-byte chunk c of LDS row r holds logical chunk c ^ swz(r), which makes both the
-// ds_read_b128 K reads and the transposing V reads bank-conflict free. The K-scale words go through registers (the
-// upper k-group reads a copy shifted by one byte). The Q fragments stay in registers.
+// K/V tiles reach a 4-slot LDS ring (the 256-thread t128 uses 3 of the slots) by direct HBM -> LDS copies
+// (buffer_load_dwordx4 ... lds); 16-byte chunk c of LDS row r holds logical chunk c ^ swz(r), which makes both the
+// ds_read_b128 K reads and the transposing V reads bank-conflict free. The 512-thread kernels stage the K-scale words
+// through registers (the upper k-group reads a copy shifted by one byte), the 256-thread kernel copies them directly.
+// The Q fragments stay in registers.
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
