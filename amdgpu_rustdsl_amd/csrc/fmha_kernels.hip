@@ -799,6 +799,11 @@ struct Wave {
         v8i qf1;
         v8i ones;
         float mx = -1.0e30f;
+        // The row max of S(t+1) in eighths behind the PV MFMAs (four accumulators: the 256-row blocks; the last eighth
+        // after the last MFMA) rather than in quarters behind the first four: fewer VALU instructions between two MFMAs
+        // of this wave, which the other wave's conversions hold up (cfg2 -0.6 %, cfg3 -0.4 %; the split-tile blocks'
+        // two accumulators keep the quarters, +3 % at cfg4 in eighths).
+        constexpr bool kSpread = NA == 4;
         if (!QK) {
 #pragma unroll
             for (int i = I0; i < I0 + DEPTH; ++i) ring[i % (DEPTH + 1)] = fetch(i);
@@ -824,12 +829,22 @@ struct Wave {
             }
             __builtin_amdgcn_sched_barrier(0);
             // row max of S(t+1): accumulator a behind PV MFMA NQ + 1 + a (accumulator a's last QK MFMA is i = NA + a)
-            if (QK && i >= NQ + 1 && i <= NQ + NA) {
+            if (QK && !kSpread && i >= NQ + 1 && i <= NQ + NA) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[i - NQ - 1][e]);
                 asm volatile("" : "+v"(mx));   // pins this quarter here (the reduction would otherwise sink past the MFMAs)
             }
+            if (QK && kSpread && i >= NQ + 1 && i <= NQ + 2 * NA - 1) {
+                const int j = i - NQ - 1;   // half-accumulator j: 8 values behind PV MFMA NQ + 1 + j, the last after the loop
+#pragma unroll
+                for (int e = 0; e < 8; ++e) mx = fmaxf(mx, s[j >> 1][8 * (j & 1) + e]);
+                asm volatile("" : "+v"(mx));
+            }
             __builtin_amdgcn_sched_barrier(0);
+        }
+        if (QK && kSpread) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, s[NA - 1][8 + e]);
         }
         if (!QK) return 0.0f;
         const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx), __builtin_bit_cast(uint32_t, mx), false, false);
