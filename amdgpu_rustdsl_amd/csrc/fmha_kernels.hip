@@ -910,13 +910,21 @@ struct Wave {
             __builtin_amdgcn_sched_barrier(0);
             after_mfma(i);
             if (QK && i < NQ && (i & 1) == 0) convert_p<LUT>(rc, sc[i >> 1], pw[i >> 1]);
-            // row max of S(t+1): accumulator a a quarter behind its last QK MFMA (i = 4 + a)
-            if (QK && i >= NQ + 1 && i <= NQ + 4) {
+            // row max of S(t+1), half an accumulator at a time: half j behind PV MFMA NQ + 1 + j (accumulator j / 2's last
+            // QK MFMA is i = 4 + j / 2)
+            // (eighths behind the PV MFMAs, the last after them, rather than quarters behind the first four: the
+            // published t128 shapes -0.5 %, cfg1 -1.5 %)
+            if (QK && i >= NQ + 1 && i <= NQ + 7) {
+                const int j = i - NQ - 1;
 #pragma unroll
-                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sn[i - NQ - 1][e]);
+                for (int e = 0; e < 8; ++e) mx = fmaxf(mx, sn[j >> 1][8 * (j & 1) + e]);
                 asm volatile("" : "+v"(mx));
             }
             __builtin_amdgcn_sched_barrier(0);
+        }
+        if (QK) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, sn[3][8 + e]);
         }
         if (!QK) return 0.0f;
         const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mx), __builtin_bit_cast(uint32_t, mx), false, false);
